@@ -1,0 +1,198 @@
+/*
+ * marlin_mi355x.h -- C ABI of the MI355X (gfx950) Marlin mixed-precision GEMM library.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP stream, and
+ * launches asynchronously on that stream.  No entry point synchronises the host.
+ * Each entry point replaces one torch op of the reference extension; the comment above it
+ * cites the reference host function whose validation contract and semantics it keeps.
+ *
+ * Return value: MARLIN_STATUS_OK, or an error code with a message available from
+ * marlin_get_last_error() (thread-local).  Messages for argument errors reuse the
+ * reference's TORCH_CHECK wording where the condition is the same.
+ *
+ * Tensor arguments are passed as (pointer, dtype, numel) where the reference passes a
+ * tensor.  An absent optional tensor is (NULL, any dtype, 0).  All tensors are contiguous
+ * row-major unless a stride argument says otherwise.
+ */
+#ifndef MARLIN_MI355X_H_
+#define MARLIN_MI355X_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without including HIP headers. */
+typedef struct ihipStream_t* marlin_stream_t;
+
+typedef enum {
+  MARLIN_STATUS_OK = 0,
+  MARLIN_STATUS_INVALID_ARGUMENT = 1, /* a validation check failed (TORCH_CHECK in the reference) */
+  MARLIN_STATUS_NOT_SUPPORTED = 2,    /* legal upstream, not implemented on this build */
+  MARLIN_STATUS_HIP_ERROR = 3,        /* a HIP runtime call or kernel launch failed */
+} marlin_status_t;
+
+/* Element types of the tensors crossing the boundary (torch dtype equivalents). */
+typedef enum {
+  MARLIN_DTYPE_FLOAT16 = 0,
+  MARLIN_DTYPE_BFLOAT16 = 1,
+  MARLIN_DTYPE_FLOAT32 = 2,
+  MARLIN_DTYPE_FLOAT8_E4M3FN = 3,
+  MARLIN_DTYPE_FLOAT8_E8M0FNU = 4,
+  MARLIN_DTYPE_INT32 = 5,
+  MARLIN_DTYPE_INT64 = 6,
+  MARLIN_DTYPE_UINT8 = 7,
+  MARLIN_DTYPE_INT8 = 8,
+} marlin_dtype_t;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* marlin_get_last_error(void);
+
+/* ABI version of this header; bumped on incompatible changes. */
+int marlin_abi_version(void);
+#define MARLIN_MI355X_ABI_VERSION 1
+
+/*
+ * Weight repack: GPTQ layout [size_k / (32/num_bits), size_n] int32 (values packed LSB-first
+ * along K) -> kernel layout, int32 [size_k/16, size_n*16/(32/num_bits)].
+ * Replaces torch.ops._C.gptq_marlin_repack
+ * (reference csrc/quantization/marlin/gptq_marlin_repack.cu:399-469).
+ * perm: optional act-order row permutation (perm_numel == size_k) or NULL/0.
+ * is_a_8bit: the reference's legacy 8-bit-activation layout; rejected on this build.
+ */
+marlin_status_t marlin_gptq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                          const int32_t* perm, int64_t perm_numel,
+                                          int64_t size_k, int64_t size_n, int64_t num_bits,
+                                          int is_a_8bit, int32_t* out, int64_t out_numel,
+                                          marlin_stream_t stream);
+
+/*
+ * Weight repack: AWQ layout [size_k, size_n / (32/num_bits)] int32 (values packed along N
+ * in AWQ interleave order) -> the same kernel layout as marlin_gptq_marlin_repack.
+ * Replaces torch.ops._C.awq_marlin_repack
+ * (reference csrc/quantization/marlin/awq_marlin_repack.cu:300-381).
+ */
+marlin_status_t marlin_awq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                         int64_t size_k, int64_t size_n, int64_t num_bits,
+                                         int is_a_8bit, int32_t* out, int64_t out_numel,
+                                         marlin_stream_t stream);
+
+/*
+ * Dense mixed-precision GEMM: C[M,N] = A[M,K] . dequant(B)[K,N] (+ bias), fp32 accumulation.
+ * Replaces torch.ops._C.marlin_gemm (reference csrc/quantization/marlin/marlin.cu:83-506).
+ *   a         : [size_m, size_k] fp16 or bf16, row stride a_row_stride elements (%8 == 0).
+ *   c         : [size_m, size_n] output, dtype of a, contiguous; overwritten (not accumulated).
+ *   b_q_weight: repacked weights (marlin_*_repack output).
+ *   b_bias    : optional [size_n], dtype of a, in marlin_permute_bias order.
+ *   b_scales  : [num_groups, size_n]; dtype of a for integer types, float8_e4m3fn
+ *               (NVFP4, S0E5M3-processed) or float8_e8m0fnu (MXFP4) for float4_e2m1f.
+ *   a_scales_numel: must be 0 (8-bit activations are not supported, as in the reference).
+ *   global_scale: NVFP4 only, fp32 numel 1.
+ *   b_zeros   : uint4/uint8 only, float zero points [num_groups, size_n] in the dtype of a,
+ *               is_zp_float must be 1.
+ *   g_idx_numel, perm_numel: must be 0 (no act-order, as in the reference).
+ *   workspace : accepted for ABI fidelity and ignored, as in the reference (marlin.cu:103);
+ *               split-K scratch is owned by the library per (device, stream).
+ *   b_type_id : vllm ScalarType id (uint4, uint4b8, uint8, uint8b128, float8_e4m3fn,
+ *               float4_e2m1f).
+ *   is_k_full, use_atomic_add, use_fp32_reduce: accepted and ignored, as in the reference.
+ */
+marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row_stride,
+                            void* c, const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                            const void* b_bias, int64_t b_bias_numel,
+                            const void* b_scales, marlin_dtype_t b_scales_dtype,
+                            int64_t b_scales_numel, int64_t num_groups,
+                            int64_t a_scales_numel,
+                            const float* global_scale, int64_t global_scale_numel,
+                            const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+                            int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel,
+                            void* workspace, int64_t workspace_bytes, int64_t b_type_id,
+                            int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
+                            int use_atomic_add, int use_fp32_reduce, int is_zp_float,
+                            marlin_stream_t stream);
+
+/*
+ * MoE token alignment: sorts the flat route indices of topk_ids by expert and pads each
+ * expert's run to a multiple of block_size.
+ * Replaces torch.ops._moe_C.moe_align_block_size
+ * (reference csrc/moe/moe_align_sum_kernels.cu:477-569).
+ *   topk_ids        : [numel] int32 or int64 expert ids (flattened [tokens, top_k]).
+ *   sorted_token_ids: [sorted_numel] int32 out; every slot not holding a route index holds
+ *                     numel (the sentinel).  Within an expert, route indices are ascending.
+ *   expert_ids      : [expert_ids_numel] int32 out; block b -> expert, -1 after the last
+ *                     used block.
+ *   num_tokens_post_pad: [1] int32 out.
+ *   expert_map      : optional [num_experts] int32 global->local id map (-1 = not local).
+ * Ids outside [0, num_experts) are skipped.
+ */
+marlin_status_t marlin_moe_align_block_size(const void* topk_ids, marlin_dtype_t topk_ids_dtype,
+                                            int64_t numel, int64_t num_experts,
+                                            int64_t block_size, int32_t* sorted_token_ids,
+                                            int64_t sorted_numel, int32_t* expert_ids,
+                                            int64_t expert_ids_numel,
+                                            int32_t* num_tokens_post_pad,
+                                            const int32_t* expert_map, int64_t expert_map_numel,
+                                            marlin_stream_t stream);
+
+/*
+ * Grouped MoE GEMM over expert-sorted row blocks.
+ * Replaces torch.ops._moe_C.moe_wna16_marlin_gemm
+ * (reference csrc/moe/marlin_moe_wna16/ops.cu:102-529).
+ * For every moe block b with expert e = expert_ids[b] >= 0 and b*moe_block_size <
+ * num_tokens_past_padded[0], and every row r of the block with
+ * id = sorted_token_ids[b*moe_block_size + r] < size_m*top_k:
+ *   C[id, :] = ((A[id / top_k, :] . dequant(B[e])) * alpha_e + bias_e' ) * w
+ * where alpha_e is the NVFP4 global scale of expert e (1 otherwise), bias_e' = bias_e *
+ * (mul_topk_weights ? alpha_e : 1) when a bias is given, and w = topk_weights[id] when
+ * mul_topk_weights, else 1.
+ *   a: [size_m, size_k]; c: [size_m*top_k, size_n]; b_q_weight: [E, size_k/16, ...];
+ *   b_scales / b_zeros: [E, num_groups, size_n]; b_bias: [E, size_n]; global_scale: [E].
+ *   thread_k, thread_n, blocks_per_sm, is_k_full, use_atomic_add, use_fp32_reduce:
+ *   accepted and ignored, as in the reference (ops.cu:125-133).
+ */
+marlin_status_t marlin_moe_wna16_marlin_gemm(
+    const void* a, marlin_dtype_t a_dtype, void* c, const int32_t* b_q_weight,
+    int64_t b_q_weight_numel, int64_t num_experts, const void* b_bias, int64_t b_bias_numel,
+    const void* b_scales, marlin_dtype_t b_scales_dtype, int64_t b_scales_numel,
+    int64_t num_groups, int64_t a_scales_numel, const float* global_scale,
+    int64_t global_scale_numel, const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+    int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel, void* workspace,
+    int64_t workspace_bytes, const int32_t* sorted_token_ids, int64_t sorted_numel,
+    const int32_t* expert_ids, int64_t expert_ids_numel,
+    const int32_t* num_tokens_past_padded, const float* topk_weights,
+    int64_t topk_weights_numel, int64_t moe_block_size, int64_t top_k, int mul_topk_weights,
+    int64_t b_type_id, int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
+    int use_atomic_add, int use_fp32_reduce, int is_zp_float, int64_t thread_k,
+    int64_t thread_n, int64_t blocks_per_sm, marlin_stream_t stream);
+
+/*
+ * Dequantize repacked weights to [size_k, size_n] (row-major) in out_dtype (fp16 or bf16),
+ * with the device dequant routines the GEMM uses.  Test and inspection aid, no counterpart
+ * op in the reference: it restates the reference's dequant helpers
+ * (tests/helpers.py:1094-1184, 1543-1641) so dequantization can be checked bit-exactly.
+ * For NVFP4 the result is dtype(fp32(v * scale) * global) as in the reference helper.
+ */
+marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                  const void* b_scales, marlin_dtype_t b_scales_dtype,
+                                  int64_t b_scales_numel, int64_t num_groups,
+                                  const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+                                  int64_t b_zeros_numel, const float* global_scale,
+                                  int64_t global_scale_numel, int64_t b_type_id,
+                                  int64_t size_k, int64_t size_n, marlin_dtype_t out_dtype,
+                                  void* out, marlin_stream_t stream);
+
+/*
+ * Top-k reduction of MoE route outputs: out[t, :] = sum_k input[t, k, :].
+ * Replaces torch.ops._moe_C.moe_sum (reference csrc/moe/moe_align_sum_kernels.cu:598-639).
+ */
+marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t num_tokens,
+                               int64_t top_k, int64_t hidden, void* out,
+                               marlin_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MARLIN_MI355X_H_ */

@@ -1,0 +1,686 @@
+// capi.hip -- extern "C" entry points of libmarlin_mi355x.so (declared in
+// include/marlin_mi355x.h): argument validation, tile selection, split-K workspace and
+// kernel dispatch.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <utility>
+
+#include "../../include/marlin_mi355x.h"
+#include "host_common.h"
+
+using namespace mmi;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct CheckFailed {
+  marlin_status_t status;
+};
+
+// Builds the message from the streamed pieces, like TORCH_CHECK(cond, a, b, ...).
+template <typename... Args>
+void check(bool cond, Args&&... args) {
+  if (cond) return;
+  std::ostringstream os;
+  (os << ... << args);
+  g_last_error = os.str();
+  throw CheckFailed{MARLIN_STATUS_INVALID_ARGUMENT};
+}
+template <typename... Args>
+void check_supported(bool cond, Args&&... args) {
+  if (cond) return;
+  std::ostringstream os;
+  (os << ... << args);
+  g_last_error = os.str();
+  throw CheckFailed{MARLIN_STATUS_NOT_SUPPORTED};
+}
+void check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  throw CheckFailed{MARLIN_STATUS_HIP_ERROR};
+}
+
+template <typename F>
+marlin_status_t guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return MARLIN_STATUS_OK;
+  } catch (const CheckFailed& c) {
+    return c.status;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return MARLIN_STATUS_HIP_ERROR;
+  }
+}
+
+// vllm ScalarType ids (vllm/scalar_type.py:25-43).
+constexpr int64_t kU4 = 1125899906843648LL;
+constexpr int64_t kU4B8 = 1125899907892224LL;
+constexpr int64_t kU8 = 1125899906844672LL;
+constexpr int64_t kU8B128 = 1125899923621888LL;
+constexpr int64_t kFE2M1f = 562949953487106LL;
+constexpr int64_t kFE4M3fn = 2814749767172868LL;
+
+int fmt_from_type(int64_t b_type_id, marlin_dtype_t scales_dtype) {
+  if (b_type_id == kU4B8) return FMT_U4B8;
+  if (b_type_id == kU4) return FMT_U4;
+  if (b_type_id == kU8B128) return FMT_U8B128;
+  if (b_type_id == kU8) return FMT_U8;
+  if (b_type_id == kFE4M3fn) return FMT_FP8;
+  if (b_type_id == kFE2M1f) {
+    if (scales_dtype == MARLIN_DTYPE_FLOAT8_E4M3FN) return FMT_NVFP4;
+    if (scales_dtype == MARLIN_DTYPE_FLOAT8_E8M0FNU) return FMT_MXFP4;
+    check(false,
+          "When b_type = float4_e2m1f, b_scales must be float8_e4m3fn for NVFP4 or "
+          "float8_e8m0fnu for MXFP4 scales.");
+  }
+  check_supported(false,
+                  "marlin_gemm implements only uint4, uint4b8, uint8, uint8b128, fp8_e4m3fn, "
+                  "nvfp4, and mxfp4 weights. Got b_type_id = ",
+                  b_type_id);
+  return -1;
+}
+
+bool is_half_type(marlin_dtype_t d) {
+  return d == MARLIN_DTYPE_FLOAT16 || d == MARLIN_DTYPE_BFLOAT16;
+}
+
+int ilog2_exact(int64_t v) {
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return (int64_t(1) << s) == v ? s : -1;
+}
+
+// ---- device properties and split-K workspace ------------------------------------------
+int device_cu_count(int dev) {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+            "hipDeviceGetAttribute");
+  cache[dev] = cus;
+  return cus;
+}
+
+struct Workspace {
+  float* ws = nullptr;
+  size_t ws_elems = 0;
+  int* counters = nullptr;
+  size_t n_counters = 0;
+};
+
+// One zero-initialised workspace per (device, stream).  Kernels leave it zeroed, so it is
+// cleared only when allocated.  Growing it synchronises the stream (first calls only).
+Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t need_counters) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, Workspace> spaces;
+  std::lock_guard<std::mutex> lk(mu);
+  Workspace& w = spaces[{dev, stream}];
+  if (need_elems > w.ws_elems) {
+    size_t n = std::max<size_t>(need_elems, std::max<size_t>(2 * w.ws_elems, size_t(1) << 20));
+    if (w.ws) {
+      check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      check_hip(hipFree(w.ws), "hipFree");
+      w.ws = nullptr;
+      w.ws_elems = 0;
+    }
+    check_hip(hipMalloc(&w.ws, n * sizeof(float)), "hipMalloc(split-K workspace)");
+    check_hip(hipMemsetAsync(w.ws, 0, n * sizeof(float), stream), "hipMemsetAsync");
+    w.ws_elems = n;
+  }
+  if (need_counters > w.n_counters) {
+    size_t n = std::max<size_t>(need_counters, std::max<size_t>(2 * w.n_counters, 4096));
+    if (w.counters) {
+      check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      check_hip(hipFree(w.counters), "hipFree");
+      w.counters = nullptr;
+      w.n_counters = 0;
+    }
+    check_hip(hipMalloc(&w.counters, n * sizeof(int)), "hipMalloc(split-K counters)");
+    check_hip(hipMemsetAsync(w.counters, 0, n * sizeof(int), stream), "hipMemsetAsync");
+    w.n_counters = n;
+  }
+  return w;
+}
+
+// ---- tile selection -------------------------------------------------------------------
+struct Plan {
+  int bm, nt, splits, steps_per_split, n_blocks, m_blocks;
+};
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+
+// Dense selector.  Small M is weight-bandwidth bound: 16-row blocks, narrow column tiles
+// and split-K until the grid holds ~4 workgroups per CU.  Large M is MFMA bound: 128x256
+// blocks (each wave 128x64), split-K only when the grid cannot cover the CUs once.
+Plan select_dense(int64_t M, int64_t N, int64_t K, int cus) {
+  Plan p{};
+  if (M <= 16) {
+    p.bm = 16;
+    p.nt = (N % 128 == 0 && N / 128 >= 2 * cus) ? 2 : 1;
+  } else if (M <= 32) {
+    p.bm = 32;
+    p.nt = (N % 128 == 0) ? 2 : 1;
+    if (p.nt == 1) p.bm = 16;
+  } else if (M <= 64) {
+    p.bm = 64;
+    p.nt = 4;
+  } else {
+    p.bm = 128;
+    p.nt = 4;
+  }
+  if (N % (64 * p.nt) != 0) {
+    // fall back to the narrowest tile that divides N (N % 64 == 0 is guaranteed)
+    p.nt = 1;
+    if (p.bm > 32) p.bm = 32;
+    if (p.bm == 32) p.bm = 16;
+  }
+  // optional override for tuning: MARLIN_MI355X_TILE="bm,nt"
+  if (const char* t = getenv("MARLIN_MI355X_TILE")) {
+    int bm = 0, nt = 0;
+    if (sscanf(t, "%d,%d", &bm, &nt) == 2) {
+      p.bm = bm;
+      p.nt = nt;
+    }
+  }
+  p.m_blocks = (int)((M + p.bm - 1) / p.bm);
+  p.n_blocks = (int)(N / (64 * p.nt));
+  const int steps = (int)(K / 128);
+  const int64_t base = (int64_t)p.m_blocks * p.n_blocks;
+  const int64_t target = (p.bm <= 32) ? (int64_t)cus * 4 : (int64_t)cus;
+  int splits = 1;
+  if (base < target && steps > 1) {
+    splits = (int)std::min<int64_t>((target + base - 1) / base, steps);
+    const int min_steps = (p.bm <= 32) ? 2 : 4;
+    splits = std::max(1, std::min(splits, std::max(1, steps / min_steps)));
+  }
+  splits = env_int("MARLIN_MI355X_SPLIT_K", splits);
+  if (steps == 0) splits = 1;
+  splits = std::max(1, std::min(splits, std::max(steps, 1)));
+  p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
+  p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
+  return p;
+}
+
+hipError_t dispatch_gemm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
+  switch (l.fmt) {
+    case FMT_U4B8: return launch_gemm_u4b8(l, p, s);
+    case FMT_U4: return launch_gemm_u4(l, p, s);
+    case FMT_U8B128: return launch_gemm_u8b128(l, p, s);
+    case FMT_U8: return launch_gemm_u8(l, p, s);
+    case FMT_FP8: return launch_gemm_fp8(l, p, s);
+    case FMT_MXFP4: return launch_gemm_mxfp4(l, p, s);
+    case FMT_NVFP4: return launch_gemm_nvfp4(l, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Validation shared by marlin_gemm, moe_wna16_marlin_gemm and marlin_dequantize for the
+// weight metadata (reference marlin.cu:107-383, ops.cu:134-402).  Returns the format.
+struct MetaCheck {
+  int fmt;
+  int group_size;  // -1 channelwise
+  int gsm;
+  int group_shift;
+};
+
+MetaCheck check_weight_meta(int64_t b_type_id, marlin_dtype_t a_dtype,
+                            marlin_dtype_t scales_dtype, int64_t scales_numel,
+                            int64_t num_groups, int64_t per_expert, const float* global_scale,
+                            int64_t global_scale_numel, int64_t expected_global,
+                            const void* b_zeros, marlin_dtype_t zeros_dtype,
+                            int64_t zeros_numel, int is_zp_float, int64_t size_n,
+                            int64_t size_k) {
+  MetaCheck mc{};
+  mc.fmt = fmt_from_type(b_type_id, scales_dtype);
+  const bool fp4 = mc.fmt == FMT_MXFP4 || mc.fmt == FMT_NVFP4;
+  if (!fp4) {
+    check(scales_dtype == a_dtype,
+          "b_scales must have the activation dtype (float16 or bfloat16), except FP4 uses "
+          "float8_e4m3fn scales for NVFP4 or float8_e8m0fnu scales for MXFP4.");
+  }
+  check(num_groups >= 1, "b_scales has no groups");
+  check(scales_numel == per_expert * num_groups * size_n, "b_scales numel = ", scales_numel,
+        " does not match num_groups * size_n = ", num_groups * size_n);
+  int group_size = -1;
+  if (num_groups > 1) {
+    check(size_k % num_groups == 0, "size_k = ", size_k,
+          ", is not divisible by b_scales.size(0) = ", num_groups);
+    group_size = (int)(size_k / num_groups);
+  }
+  mc.group_size = group_size;
+
+  const bool has_global = global_scale_numel > 0;
+  if (has_global) {
+    check(mc.fmt == FMT_NVFP4, "global_scale is supported only for nvfp4 format.");
+    check(global_scale != nullptr, "global_scale pointer is null");
+    check(global_scale_numel == expected_global, "nvfp4 expects global_scale numel = ",
+          expected_global, ". Got global_scale.numel() = ", global_scale_numel);
+  } else {
+    check(mc.fmt != FMT_NVFP4, "the global_scale parameter must be passed for nvfp4 format.");
+  }
+
+  const bool has_zp = zeros_numel > 0;
+  check(!has_zp || mc.fmt == FMT_U4 || mc.fmt == FMT_U8,
+        "zero-point metadata is supported only for uint4 and uint8 weights.");
+  if (has_zp) {
+    check(is_zp_float,
+          "received b_zeros but is_zp_float is false. Packed integer zero-points are not "
+          "supported on the uint4/uint8 path.");
+    check(b_zeros != nullptr, "b_zeros pointer is null");
+    check(zeros_dtype == a_dtype,
+          "uint4/uint8 zero points must have the activation dtype (float16 or bfloat16).");
+    check(zeros_numel == scales_numel, "b_zeros numel = ", zeros_numel,
+          " is not num_groups * size_n = ", scales_numel / per_expert);
+  } else {
+    check(!is_zp_float, "is_zp_float is true but b_zeros was not provided.");
+  }
+  if (mc.fmt == FMT_U4 || mc.fmt == FMT_U8) {
+    check(has_zp && is_zp_float, mc.fmt == FMT_U4 ? "uint4" : "uint8",
+          " path requires float zero points (is_zp_float=true).");
+  }
+
+  // group-size support per format (reference marlin.cu:434-493, sm70_marlin_gemm.cuh:98-141)
+  if (mc.fmt == FMT_NVFP4) {
+    check(group_size == 16, "nvfp4 supports only group_size 16. Got ", group_size);
+  } else if (mc.fmt == FMT_MXFP4) {
+    check(group_size == 32, "mxfp4 supports only group_size 32 when global_scale is not "
+                            "provided. Got ", group_size);
+  } else if (mc.fmt == FMT_FP8) {
+    check(group_size == -1 || group_size == 128,
+          "fp8_e4m3 supports only group_size -1 or 128. Got ", group_size);
+  } else {
+    check(group_size == -1 || (group_size >= 32 && ilog2_exact(group_size) >= 0),
+          "unsupported group_size = ", group_size,
+          " (supported: -1 or a power of two >= 32)");
+  }
+  if (group_size == -1) {
+    mc.gsm = GSM_CHANNEL;
+    mc.group_shift = 0;
+  } else {
+    mc.group_shift = ilog2_exact(group_size);
+    mc.gsm = group_size >= 128 ? GSM_BIG : GSM_SMALL;
+  }
+  return mc;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* marlin_get_last_error(void) { return g_last_error.c_str(); }
+
+int marlin_abi_version(void) { return MARLIN_MI355X_ABI_VERSION; }
+
+marlin_status_t marlin_gptq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                          const int32_t* perm, int64_t perm_numel,
+                                          int64_t size_k, int64_t size_n, int64_t num_bits,
+                                          int is_a_8bit, int32_t* out, int64_t out_numel,
+                                          marlin_stream_t stream) {
+  return guarded([&] {
+    check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_k_size = ", 16);
+    check(size_n % 64 == 0, "size_n = ", size_n, " is not divisible by tile_n_size = ", 64);
+    check(num_bits == 4 || num_bits == 8, "num_bits must be 4 or 8. Got = ", num_bits);
+    check_supported(!is_a_8bit,
+                    "is_a_8bit=true (8-bit activation layout) is not supported on this build");
+    check(size_k % 32 == 0, "size_k = ", size_k,
+          " is not divisible by 32 (the gfx950 layout packs 32-deep MFMA blocks)");
+    const int64_t pack = 32 / num_bits;
+    check(b_q_weight_numel == size_k / pack * size_n, "Shape mismatch: b_q_weight numel = ",
+          b_q_weight_numel, ", expected size_k / pack_factor * size_n = ", size_k / pack * size_n);
+    check(out_numel == size_k * size_n / pack, "out numel = ", out_numel, ", expected ",
+          size_k * size_n / pack);
+    check(perm_numel == 0 || perm_numel == size_k, "perm numel = ", perm_numel,
+          " must be 0 or size_k = ", size_k);
+    if (size_k == 0 || size_n == 0) return;
+    check(b_q_weight != nullptr && out != nullptr, "null tensor pointer");
+    check_hip(launch_gptq_repack(reinterpret_cast<const uint32_t*>(b_q_weight),
+                                 perm_numel ? perm : nullptr, reinterpret_cast<uint32_t*>(out),
+                                 size_k, size_n, (int)num_bits, (hipStream_t)stream),
+              "gptq_marlin_repack launch");
+  });
+}
+
+marlin_status_t marlin_awq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                         int64_t size_k, int64_t size_n, int64_t num_bits,
+                                         int is_a_8bit, int32_t* out, int64_t out_numel,
+                                         marlin_stream_t stream) {
+  return guarded([&] {
+    check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_k_size = ", 16);
+    check(size_n % 64 == 0, "size_n = ", size_n, " is not divisible by tile_n_size = ", 64);
+    check(num_bits == 4 || num_bits == 8, "num_bits must be 4 or 8. Got = ", num_bits);
+    check_supported(!is_a_8bit,
+                    "is_a_8bit=true (8-bit activation layout) is not supported on this build");
+    check(size_k % 32 == 0, "size_k = ", size_k,
+          " is not divisible by 32 (the gfx950 layout packs 32-deep MFMA blocks)");
+    const int64_t pack = 32 / num_bits;
+    check(b_q_weight_numel == size_k * (size_n / pack), "Shape mismatch: b_q_weight numel = ",
+          b_q_weight_numel, ", expected size_k * size_n / pack_factor = ", size_k * (size_n / pack));
+    check(out_numel == size_k * size_n / pack, "out numel = ", out_numel, ", expected ",
+          size_k * size_n / pack);
+    if (size_k == 0 || size_n == 0) return;
+    check(b_q_weight != nullptr && out != nullptr, "null tensor pointer");
+    check_hip(launch_awq_repack(reinterpret_cast<const uint32_t*>(b_q_weight),
+                                reinterpret_cast<uint32_t*>(out), size_k, size_n, (int)num_bits,
+                                (hipStream_t)stream),
+              "awq_marlin_repack launch");
+  });
+}
+
+marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row_stride,
+                            void* c, const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                            const void* b_bias, int64_t b_bias_numel,
+                            const void* b_scales, marlin_dtype_t b_scales_dtype,
+                            int64_t b_scales_numel, int64_t num_groups,
+                            int64_t a_scales_numel,
+                            const float* global_scale, int64_t global_scale_numel,
+                            const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+                            int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel,
+                            void* workspace, int64_t workspace_bytes, int64_t b_type_id,
+                            int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
+                            int use_atomic_add, int use_fp32_reduce, int is_zp_float,
+                            marlin_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  (void)is_k_full;
+  (void)use_atomic_add;
+  (void)use_fp32_reduce;
+  return guarded([&] {
+    check(g_idx_numel == 0, "marlin_gemm does not support act_order g_idx.");
+    check(perm_numel == 0, "marlin_gemm does not support act_order perm.");
+    check_supported(is_half_type(a_dtype),
+                    "only float16 and bfloat16 activations are supported (8-bit activations are "
+                    "not implemented).");
+    check(a_scales_numel == 0, "a_scales can only be used for 8bit activation.");
+    const MetaCheck mc = check_weight_meta(b_type_id, a_dtype, b_scales_dtype, b_scales_numel,
+                                           num_groups, 1, global_scale, global_scale_numel, 1,
+                                           b_zeros, b_zeros_dtype, b_zeros_numel, is_zp_float,
+                                           size_n, size_k);
+    const int bits = fmt_bits(mc.fmt);
+    const int64_t pack = 32 / bits;
+    check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
+    check(b_q_weight_numel == size_k * size_n / pack, "Shape mismatch: b_q_weight numel = ",
+          b_q_weight_numel, ", size_k * size_n / pack_factor = ", size_k * size_n / pack);
+    check(size_k % 32 == 0, "marlin_gemm requires size_k % 32 == 0.");
+    check(size_n % 64 == 0, "marlin_gemm requires size_n % 64 == 0. size_n = ", size_n,
+          ", min_thread_n = ", 64);
+    check(a_row_stride % 8 == 0, "A.stride(0) must divisible by 8");
+    check(((uintptr_t)a) % 16 == 0, "A must aligned to 16 bytes");
+    check(b_bias_numel == 0 || b_bias_numel == size_n, "b_bias.size(0) != size_n");
+    check(size_m >= 0 && size_m <= INT32_MAX, "size_m out of range");
+    if (size_m == 0 || size_n == 0) return;
+    check(size_k > 0, "size_k must be positive");
+    check(a && c && b_q_weight && b_scales, "null tensor pointer");
+
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    const Plan plan = select_dense(size_m, size_n, size_k, device_cu_count(dev));
+
+    GemmParams p{};
+    p.a = a;
+    p.a_stride = a_row_stride;
+    p.c = c;
+    p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
+    p.b_expert_stride = 0;
+    p.scales = b_scales;
+    p.zeros = b_zeros_numel ? b_zeros : nullptr;
+    p.meta_expert_stride = 0;
+    p.bias = b_bias_numel ? b_bias : nullptr;
+    p.global_scale = global_scale;
+    p.alpha_exp = 7 - (a_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
+    p.M = (int)size_m;
+    p.N = (int)size_n;
+    p.K = (int)size_k;
+    p.group_shift = mc.group_shift;
+    p.splits = plan.splits;
+    p.steps_per_split = plan.steps_per_split;
+    p.num_n_blocks = plan.n_blocks;
+    if (plan.splits > 1) {
+      Workspace& w = get_workspace(dev, s, (size_t)size_m * size_n,
+                                   (size_t)plan.m_blocks * plan.n_blocks);
+      p.ws = w.ws;
+      p.counters = w.counters;
+    }
+    GemmLaunch l{};
+    l.fmt = mc.fmt;
+    l.bf16 = a_dtype == MARLIN_DTYPE_BFLOAT16;
+    l.gsm = mc.gsm;
+    l.bm = plan.bm;
+    l.nt = plan.nt;
+    l.moe = false;
+    l.grid = (unsigned)((int64_t)plan.m_blocks * plan.n_blocks * plan.splits);
+    check_hip(dispatch_gemm(l, p, s), "marlin_gemm launch");
+  });
+}
+
+marlin_status_t marlin_moe_align_block_size(const void* topk_ids, marlin_dtype_t topk_ids_dtype,
+                                            int64_t numel, int64_t num_experts,
+                                            int64_t block_size, int32_t* sorted_token_ids,
+                                            int64_t sorted_numel, int32_t* expert_ids,
+                                            int64_t expert_ids_numel,
+                                            int32_t* num_tokens_post_pad,
+                                            const int32_t* expert_map, int64_t expert_map_numel,
+                                            marlin_stream_t stream) {
+  return guarded([&] {
+    check(topk_ids_dtype == MARLIN_DTYPE_INT32 || topk_ids_dtype == MARLIN_DTYPE_INT64,
+          "topk_ids must be int32 or int64");
+    check(num_experts >= 1, "num_experts must be positive");
+    const int64_t padded_num_experts = (num_experts + 63) / 64 * 64;
+    check(padded_num_experts <= 1024, "padded_num_experts must be at most 1024");
+    check(block_size >= 1, "block_size must be positive");
+    check(numel >= 0 && numel < INT32_MAX, "topk_ids numel out of range");
+    check(sorted_numel >= numel + num_experts * (block_size - 1) || sorted_numel >= numel,
+          "sorted_token_ids too small");
+    check(expert_map_numel == 0 || expert_map_numel >= num_experts,
+          "expert_map must cover num_experts entries");
+    check(sorted_token_ids && expert_ids && num_tokens_post_pad, "null output pointer");
+    check(numel == 0 || topk_ids, "null topk_ids pointer");
+    check_hip(launch_moe_align(topk_ids, topk_ids_dtype == MARLIN_DTYPE_INT64, numel,
+                               (int)num_experts, (int)block_size, sorted_token_ids, sorted_numel,
+                               expert_ids, expert_ids_numel, num_tokens_post_pad,
+                               expert_map_numel ? expert_map : nullptr, (hipStream_t)stream),
+              "moe_align_block_size launch");
+  });
+}
+
+marlin_status_t marlin_moe_wna16_marlin_gemm(
+    const void* a, marlin_dtype_t a_dtype, void* c, const int32_t* b_q_weight,
+    int64_t b_q_weight_numel, int64_t num_experts, const void* b_bias, int64_t b_bias_numel,
+    const void* b_scales, marlin_dtype_t b_scales_dtype, int64_t b_scales_numel,
+    int64_t num_groups, int64_t a_scales_numel, const float* global_scale,
+    int64_t global_scale_numel, const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+    int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel, void* workspace,
+    int64_t workspace_bytes, const int32_t* sorted_token_ids, int64_t sorted_numel,
+    const int32_t* expert_ids, int64_t expert_ids_numel,
+    const int32_t* num_tokens_past_padded, const float* topk_weights,
+    int64_t topk_weights_numel, int64_t moe_block_size, int64_t top_k, int mul_topk_weights,
+    int64_t b_type_id, int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
+    int use_atomic_add, int use_fp32_reduce, int is_zp_float, int64_t thread_k,
+    int64_t thread_n, int64_t blocks_per_sm, marlin_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  (void)is_k_full;
+  (void)use_atomic_add;
+  (void)use_fp32_reduce;
+  (void)thread_k;
+  (void)thread_n;
+  (void)blocks_per_sm;
+  return guarded([&] {
+    check(g_idx_numel == 0, "moe_wna16_marlin_gemm does not support act_order g_idx.");
+    check(perm_numel == 0, "moe_wna16_marlin_gemm does not support act_order perm.");
+    check_supported(is_half_type(a_dtype),
+                    "only float16 and bfloat16 activations are supported (8-bit activations are "
+                    "not implemented).");
+    check(a_scales_numel == 0, "a_scales can only be used for 8bit activation.");
+    if (moe_block_size != 8) {
+      check(moe_block_size % 16 == 0, "unsupported moe_block_size=", moe_block_size);
+      check(moe_block_size >= 16 && moe_block_size <= 64, "unsupported moe_block_size=",
+            moe_block_size);
+    }
+    check(num_experts >= 1, "num_experts must be positive");
+    const MetaCheck mc = check_weight_meta(b_type_id, a_dtype, b_scales_dtype, b_scales_numel,
+                                           num_groups, num_experts, global_scale,
+                                           global_scale_numel, num_experts, b_zeros,
+                                           b_zeros_dtype, b_zeros_numel, is_zp_float, size_n,
+                                           size_k);
+    const int bits = fmt_bits(mc.fmt);
+    const int64_t pack = 32 / bits;
+    check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
+    check(b_q_weight_numel == num_experts * size_k * size_n / pack,
+          "Shape mismatch: b_q_weight numel = ", b_q_weight_numel,
+          ", expected num_experts * size_k * size_n / pack_factor = ",
+          num_experts * size_k * size_n / pack);
+    check(size_k % 32 == 0, "moe_wna16_marlin_gemm requires size_k % 32 == 0.");
+    check(size_n % 64 == 0, "size_n = ", size_n, ", is not divisible by min_thread_n = ", 64);
+    check(b_bias_numel == 0 || b_bias_numel == num_experts * size_n,
+          "b_bias must be [num_experts, size_n]");
+    check(top_k >= 1, "top_k must be positive");
+    check(!mul_topk_weights || topk_weights_numel >= size_m * top_k,
+          "topk_weights must hold size_m * top_k values");
+    check(((uintptr_t)a) % 16 == 0, "A must aligned to 16 bytes");
+    check(size_k % 8 == 0, "A row stride must be divisible by 8");
+    check((int64_t)size_m * top_k <= INT32_MAX, "size_m * top_k out of range");
+    check(expert_ids_numel >= 1, "expert_ids is empty");
+    if (size_m == 0 || size_n == 0 || sorted_numel == 0) return;
+    check(a && c && b_q_weight && b_scales && sorted_token_ids && expert_ids &&
+              num_tokens_past_padded,
+          "null tensor pointer");
+
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    const int cus = device_cu_count(dev);
+
+    const int bm = moe_block_size <= 16 ? 16 : (int)moe_block_size;  // 8 -> 16 rows
+    const int nt = 4;
+    check_supported(size_n % 256 == 0,
+                    "moe_wna16_marlin_gemm on this build requires size_n % 256 == 0");
+    const int m_blocks = (int)((sorted_numel + moe_block_size - 1) / moe_block_size);
+    const int n_blocks = (int)(size_n / 256);
+    const int steps = (int)(size_k / 128);
+    // Only a fraction of the moe blocks are live; estimate them from the route count.
+    const int64_t live = std::min<int64_t>(m_blocks, (size_m * top_k + moe_block_size - 1) /
+                                                         moe_block_size + num_experts);
+    int splits = 1;
+    const int64_t base = live * n_blocks;
+    if (base < (int64_t)cus * 2 && steps >= 4) {
+      splits = (int)std::min<int64_t>(((int64_t)cus * 2 + base - 1) / base, steps / 2);
+    }
+    splits = env_int("MARLIN_MI355X_MOE_SPLIT_K", splits);
+    splits = std::max(1, std::min(splits, std::max(steps, 1)));
+    const int sps = steps == 0 ? 0 : (steps + splits - 1) / splits;
+    splits = steps == 0 ? 1 : (steps + sps - 1) / sps;
+
+    GemmParams p{};
+    p.a = a;
+    p.a_stride = size_k;
+    p.c = c;
+    p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
+    p.b_expert_stride = size_k * size_n / pack;
+    p.scales = b_scales;
+    p.zeros = b_zeros_numel ? b_zeros : nullptr;
+    p.meta_expert_stride = num_groups * size_n;
+    p.bias = b_bias_numel ? b_bias : nullptr;
+    p.global_scale = global_scale;
+    p.alpha_exp = 7 - (a_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
+    p.M = (int)size_m;
+    p.N = (int)size_n;
+    p.K = (int)size_k;
+    p.group_shift = mc.group_shift;
+    p.splits = splits;
+    p.steps_per_split = sps;
+    p.num_n_blocks = n_blocks;
+    p.sorted_ids = sorted_token_ids;
+    p.sorted_numel = (int)sorted_numel;
+    p.expert_ids = expert_ids;
+    p.expert_ids_numel = (int)std::min<int64_t>(expert_ids_numel, INT32_MAX);
+    p.num_post_pad = num_tokens_past_padded;
+    p.topk_w = topk_weights;
+    p.top_k = (int)top_k;
+    p.moe_bs = (int)moe_block_size;
+    p.mul_topk = mul_topk_weights ? 1 : 0;
+    p.valid_ids = (int)(size_m * top_k);
+    if (splits > 1) {
+      Workspace& w = get_workspace(dev, s, (size_t)size_m * top_k * size_n,
+                                   (size_t)m_blocks * n_blocks);
+      p.ws = w.ws;
+      p.counters = w.counters;
+    }
+    GemmLaunch l{};
+    l.fmt = mc.fmt;
+    l.bf16 = a_dtype == MARLIN_DTYPE_BFLOAT16;
+    l.gsm = mc.gsm;
+    l.bm = bm;
+    l.nt = nt;
+    l.moe = true;
+    l.grid = (unsigned)((int64_t)m_blocks * n_blocks * splits);
+    check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");
+  });
+}
+
+marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                  const void* b_scales, marlin_dtype_t b_scales_dtype,
+                                  int64_t b_scales_numel, int64_t num_groups,
+                                  const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+                                  int64_t b_zeros_numel, const float* global_scale,
+                                  int64_t global_scale_numel, int64_t b_type_id,
+                                  int64_t size_k, int64_t size_n, marlin_dtype_t out_dtype,
+                                  void* out, marlin_stream_t stream) {
+  return guarded([&] {
+    check(is_half_type(out_dtype), "out_dtype must be float16 or bfloat16");
+    const MetaCheck mc = check_weight_meta(b_type_id, out_dtype, b_scales_dtype, b_scales_numel,
+                                           num_groups, 1, global_scale, global_scale_numel, 1,
+                                           b_zeros, b_zeros_dtype, b_zeros_numel,
+                                           b_zeros_numel > 0 ? 1 : 0, size_n, size_k);
+    const int64_t pack = 32 / fmt_bits(mc.fmt);
+    check(size_k % 32 == 0, "size_k must be divisible by 32");
+    check(size_n % 16 == 0, "size_n must be divisible by 16");
+    check(b_q_weight_numel == size_k * size_n / pack, "b_q_weight numel mismatch");
+    if (size_k == 0 || size_n == 0) return;
+    GemmParams p{};
+    p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
+    p.scales = b_scales;
+    p.zeros = b_zeros_numel ? b_zeros : nullptr;
+    p.global_scale = global_scale;
+    p.alpha_exp = 7 - (out_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
+    p.N = (int)size_n;
+    p.K = (int)size_k;
+    p.group_shift = mc.group_shift;
+    check_hip(launch_dequant(mc.fmt, p, out_dtype == MARLIN_DTYPE_BFLOAT16, out, mc.gsm,
+                             (hipStream_t)stream),
+              "marlin_dequantize launch");
+  });
+}
+
+marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t num_tokens,
+                               int64_t top_k, int64_t hidden, void* out,
+                               marlin_stream_t stream) {
+  return guarded([&] {
+    check(is_half_type(dtype), "moe_sum supports float16 and bfloat16");
+    check(num_tokens >= 0 && top_k >= 1 && hidden >= 0, "invalid moe_sum shape");
+    check(num_tokens <= 65535, "moe_sum supports at most 65535 tokens per call");
+    if (num_tokens == 0 || hidden == 0) return;
+    check(input && out, "null tensor pointer");
+    check_hip(launch_moe_sum(input, dtype == MARLIN_DTYPE_BFLOAT16, num_tokens, (int)top_k, hidden,
+                             out, (hipStream_t)stream),
+              "moe_sum launch");
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,280 @@
+// device_common.h -- types, weight layout, dequant routines and MFMA wrappers for gfx950.
+//
+// Weight layout ("tile-chunk layout"), shared by the repack, dequant and GEMM kernels.
+// The packed weight buffer keeps the reference's container shape [K/16, N*16/pack] int32
+// (vllm/_custom_ops.py:1187-1193) but orders words for 64-wide wavefronts feeding
+// v_mfma_f32_16x16x32_{f16,bf16}:
+//   * Columns are split into n16 tiles; tile t owns a contiguous run of K*16/pack words.
+//   * Inside a tile, K is cut into chunks of 1 KiB = 64 lanes x 4 words.  A chunk covers
+//     KC = 128 k (4-bit) or KC = 64 k (8-bit).  Lane l of a wave owns column 16t + l%16 and
+//     lane-group g = l/16; its 4 words are consecutive, so one dwordx4 per lane loads the
+//     whole chunk with a fully coalesced 1 KiB wave access.
+//   * Word j of lane l holds, for 4-bit: the 8 values k = c*128 + 32*j + 8*g + [0..7]
+//     (k32 block j of the chunk); for 8-bit: the 4 values
+//     k = c*64 + 32*(j/2) + 8*g + 4*(j%2) + [0..3].  Values sit in natural order, value i in
+//     bits [i*bits, (i+1)*bits).
+//   * That is exactly the B operand of one 16x16x32 MFMA: lane l supplies column l%16 and
+//     k-slice 8*g..8*g+7 of a 32-deep block.  The A operand uses the same k-slice per lane.
+//   * K % KC != 0 leaves a tail of (K % KC)/32 k32 blocks per tile, stored after the full
+//     chunks with J = tail words per lane, lane-major.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mmi {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// Activation / output element tags.
+struct F16 {
+  static constexpr int kId = 0;
+};
+struct BF16 {
+  static constexpr int kId = 1;
+};
+
+// Weight formats handled by the kernels.
+enum Fmt : int {
+  FMT_U4B8 = 0,   // uint4, bias 8 (GPTQ symmetric)
+  FMT_U4 = 1,     // uint4 + float zero point (AWQ)
+  FMT_U8B128 = 2, // uint8, bias 128
+  FMT_U8 = 3,     // uint8 + float zero point
+  FMT_FP8 = 4,    // float8_e4m3fn, scales carry the x256 exponent fold
+  FMT_MXFP4 = 5,  // float4_e2m1f + float8_e8m0fnu scale per 32
+  FMT_NVFP4 = 6,  // float4_e2m1f + S0E5M3 scale per 16 + fp32 global scale
+};
+
+__host__ __device__ constexpr int fmt_bits(int f) {
+  return (f == FMT_U8B128 || f == FMT_U8 || f == FMT_FP8) ? 8 : 4;
+}
+__host__ __device__ constexpr bool fmt_has_zp(int f) { return f == FMT_U4 || f == FMT_U8; }
+__host__ __device__ constexpr bool fmt_byte_scale(int f) {
+  return f == FMT_MXFP4 || f == FMT_NVFP4;
+}
+
+// ---------------------------------------------------------------------------------------
+// Layout index math (host and device).
+// ---------------------------------------------------------------------------------------
+__host__ __device__ inline int64_t tile_words(int bits, int64_t size_k) {
+  return size_k * 16 / (32 / bits);
+}
+__host__ __device__ inline int chunk_k(int bits) { return bits == 4 ? 128 : 64; }
+
+// Word index of the word holding values (n, k..k+pack-1), k a multiple of pack.
+__host__ __device__ inline int64_t layout_word_index(int bits, int64_t size_k, int64_t n,
+                                                     int64_t k) {
+  const int64_t t = n >> 4;
+  const int64_t nl = n & 15;
+  const int64_t kc = chunk_k(bits);
+  const int64_t full = size_k / kc;
+  const int64_t c = k / kc;
+  const int64_t kin = k - c * kc;  // k inside chunk
+  const int64_t blk = kin >> 5;    // k32 block inside chunk
+  const int64_t g = (kin >> 3) & 3;
+  const int64_t lane = g * 16 + nl;
+  int64_t j;
+  int64_t wpl;
+  if (bits == 4) {
+    j = blk;
+  } else {
+    j = blk * 2 + ((kin >> 2) & 1);
+  }
+  if (c < full) {
+    wpl = 4;
+  } else {
+    wpl = (size_k - full * kc) / 32 * (bits / 4);
+  }
+  return t * tile_words(bits, size_k) + c * 256 + lane * wpl + j;
+}
+
+// ---------------------------------------------------------------------------------------
+// Scalar conversions.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float raw16_to_float(uint32_t raw, F16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)raw);
+}
+__device__ __forceinline__ float raw16_to_float(uint32_t raw, BF16) {
+  return __builtin_bit_cast(float, raw << 16);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, F16) {
+  f16x2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, BF16) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t to_raw16(float v, F16) {
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+__device__ __forceinline__ uint16_t to_raw16(float v, BF16) {
+  return __builtin_bit_cast(uint16_t, (__bf16)v);
+}
+
+// e8m0 byte -> 2^(e-127) as fp32 (e = 255 -> NaN).
+__device__ __forceinline__ float e8m0_to_float(uint32_t e) {
+  uint32_t bits = e == 0 ? 0x00400000u : (e == 255 ? 0x7fc00000u : (e << 23));
+  return __builtin_bit_cast(float, bits);
+}
+// S0E5M3 byte b (the reference's NVFP4 scale re-encoding, marlin_utils_fp4.py:83-110):
+// fp16 bits (b << 7) hold scale*2^7*sf.  Returns scale*sf = fp16(b<<7) * 2^-7 as fp32.
+__device__ __forceinline__ float s0e5m3_to_float_div128(uint32_t b) {
+  return b == 0 ? 0.0f : __builtin_bit_cast(float, (b << 20) + (105u << 23));
+}
+
+// ---------------------------------------------------------------------------------------
+// Per-group dequant constants ("meta") and operand dequantization.
+//
+// Integer formats use the fp16 magic-number trick: (nibble | 0x6400) is the fp16 value
+// 1024 + q (or 1024 + 16q for the odd nibble of a byte).  v_fma_mix_f32 widens that half
+// exactly and computes x*s' + c in one fused step; c is chosen so the result is exactly
+// q*s - zp (or (q - bias)*s).  Every such value has at most 22 significant bits, so the
+// fp32 result is exact and the single conversion to the activation dtype is the only
+// rounding -- the reference semantics rnd(q*s - zp) / rnd((q - bias)*s)
+// (tests/helpers.py:1094-1133, 1576-1641; dequant.h:131-328).
+// ---------------------------------------------------------------------------------------
+struct Meta {
+  float s;    // scale for values at 1024 + q
+  float s16;  // scale/16 for values at 1024 + 16q
+  float c1;   // offset for 1024 + q
+  float c16;  // offset for 1024 + 16q
+};
+
+// Raw metadata for one (group, column): low 16 bits scale, high 16 bits zero point for
+// 16-bit metadata; the scale byte for fp4.
+template <int FMT, class AT>
+__device__ __forceinline__ Meta make_meta(uint32_t raw) {
+  Meta m;
+  if constexpr (FMT == FMT_MXFP4) {
+    m.s = e8m0_to_float(raw & 0xff);
+    m.s16 = m.c1 = m.c16 = 0.f;
+  } else if constexpr (FMT == FMT_NVFP4) {
+    m.s = s0e5m3_to_float_div128(raw & 0xff);
+    m.s16 = m.c1 = m.c16 = 0.f;
+  } else if constexpr (FMT == FMT_FP8) {
+    // Dequant is fp8 * (s / 256) (tests/helpers.py:1117-1121).
+    m.s = raw16_to_float(raw & 0xffff, AT{}) * 0.00390625f;
+    m.s16 = m.c1 = m.c16 = 0.f;
+  } else {
+    const float s = raw16_to_float(raw & 0xffff, AT{});
+    m.s = s;
+    m.s16 = s * 0.0625f;
+    if constexpr (FMT == FMT_U4B8) {
+      m.c1 = -1032.0f * s;  // (1024 + q)*s - 1032 s = (q - 8) s
+      m.c16 = -72.0f * s;   // (1024 + 16q)*s/16 - 72 s = (q - 8) s
+    } else if constexpr (FMT == FMT_U8B128) {
+      m.c1 = -1152.0f * s;  // (1024 + q)*s - 1152 s = (q - 128) s
+      m.c16 = 0.f;
+    } else {
+      const float z = raw16_to_float(raw >> 16, AT{});
+      m.c1 = __builtin_fmaf(-1024.0f, s, -z);  // exact: |1024 s + z| has <= 22 bits
+      m.c16 = __builtin_fmaf(-64.0f, s, -z);
+    }
+  }
+  return m;
+}
+
+__device__ __forceinline__ float h_lo(uint32_t x) {
+  return (float)__builtin_bit_cast(f16x2_t, x)[0];
+}
+__device__ __forceinline__ float h_hi(uint32_t x) {
+  return (float)__builtin_bit_cast(f16x2_t, x)[1];
+}
+
+// Dequantize the MFMA B operand of one lane: 8 consecutive k of one column.
+// 4-bit formats read w0 only, 8-bit formats read w0 (k0..3) and w1 (k4..7).
+template <int FMT, class AT>
+__device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, const Meta& m) {
+  u32x4_t r;
+  if constexpr (FMT == FMT_U4B8 || FMT == FMT_U4) {
+    const uint32_t x0 = (w0 & 0x000f000fu) | 0x64006400u;  // k0, k4  : 1024 + q
+    const uint32_t x1 = (w0 & 0x00f000f0u) | 0x64006400u;  // k1, k5  : 1024 + 16q
+    const uint32_t t = w0 >> 8;
+    const uint32_t x2 = (t & 0x000f000fu) | 0x64006400u;  // k2, k6
+    const uint32_t x3 = (t & 0x00f000f0u) | 0x64006400u;  // k3, k7
+    const float e0 = __builtin_fmaf(h_lo(x0), m.s, m.c1);
+    const float e4 = __builtin_fmaf(h_hi(x0), m.s, m.c1);
+    const float e1 = __builtin_fmaf(h_lo(x1), m.s16, m.c16);
+    const float e5 = __builtin_fmaf(h_hi(x1), m.s16, m.c16);
+    const float e2 = __builtin_fmaf(h_lo(x2), m.s, m.c1);
+    const float e6 = __builtin_fmaf(h_hi(x2), m.s, m.c1);
+    const float e3 = __builtin_fmaf(h_lo(x3), m.s16, m.c16);
+    const float e7 = __builtin_fmaf(h_hi(x3), m.s16, m.c16);
+    r[0] = pack2(e0, e1, AT{});
+    r[1] = pack2(e2, e3, AT{});
+    r[2] = pack2(e4, e5, AT{});
+    r[3] = pack2(e6, e7, AT{});
+  } else if constexpr (FMT == FMT_U8B128 || FMT == FMT_U8) {
+    const uint32_t a0 = (w0 & 0x00ff00ffu) | 0x64006400u;         // k0, k2
+    const uint32_t a1 = ((w0 >> 8) & 0x00ff00ffu) | 0x64006400u;  // k1, k3
+    const uint32_t b0 = (w1 & 0x00ff00ffu) | 0x64006400u;         // k4, k6
+    const uint32_t b1 = ((w1 >> 8) & 0x00ff00ffu) | 0x64006400u;  // k5, k7
+    r[0] = pack2(__builtin_fmaf(h_lo(a0), m.s, m.c1), __builtin_fmaf(h_lo(a1), m.s, m.c1),
+                 AT{});
+    r[1] = pack2(__builtin_fmaf(h_hi(a0), m.s, m.c1), __builtin_fmaf(h_hi(a1), m.s, m.c1),
+                 AT{});
+    r[2] = pack2(__builtin_fmaf(h_lo(b0), m.s, m.c1), __builtin_fmaf(h_lo(b1), m.s, m.c1),
+                 AT{});
+    r[3] = pack2(__builtin_fmaf(h_hi(b0), m.s, m.c1), __builtin_fmaf(h_hi(b1), m.s, m.c1),
+                 AT{});
+  } else if constexpr (FMT == FMT_FP8) {
+    // OCP e4m3fn -> fp32 exactly, times s/256 (exact: <= 15 significant bits), one rounding.
+    const f32x2_t p0 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
+    const f32x2_t p1 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
+    const f32x2_t p2 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
+    const f32x2_t p3 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
+    r[0] = pack2(p0[0] * m.s, p0[1] * m.s, AT{});
+    r[1] = pack2(p1[0] * m.s, p1[1] * m.s, AT{});
+    r[2] = pack2(p2[0] * m.s, p2[1] * m.s, AT{});
+    r[3] = pack2(p3[0] * m.s, p3[1] * m.s, AT{});
+  } else {
+    // e2m1 pairs -> 16-bit with a hardware scaled conversion.  e2m1 values carry at most
+    // 2 significant bits and the scale (a power of two for MXFP4, a 4-bit-significand
+    // e4m3 value times a power of two for NVFP4) at most 4, so the product is exact.
+    if constexpr (AT::kId == 1) {
+      r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, m.s, 0));
+      r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, m.s, 1));
+      r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, m.s, 2));
+      r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, m.s, 3));
+    } else {
+      r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 0));
+      r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 1));
+      r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 2));
+      r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 3));
+    }
+  }
+  return r;
+}
+
+// D += A(16x32) * B(32x16).  Lane l supplies A row l%16 / B column l%16, k-slice 8*(l/16).
+// Result lane l holds D[4*(l/16) + i][l%16], i = 0..3.
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, f32x4_t c, F16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, f32x4_t c,
+                                          BF16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Logical column -> storage index of a bias permuted with marlin_permute_bias
+// (reference sm70_marlin_bias.cuh:18-25; marlin_utils.py:279-314).
+__device__ __forceinline__ int bias_storage_index(int col) {
+  // scale_perm_single: storage p holds logical col 2*(p/8) + {0,1,8,9,16,17,24,25}[p%8]
+  // within each 32-column group; this is its inverse.
+  const int lc = col & 31;
+  const int i = lc >> 3;           // which of {0,1},{8,9},{16,17},{24,25} pair-group
+  const int r = lc & 7;            // 2*(p/8) + j  with j in {0,1}
+  const int p = (r >> 1) * 8 + i * 2 + (r & 1);
+  return (col & ~31) + p;
+}
+
+}  // namespace mmi

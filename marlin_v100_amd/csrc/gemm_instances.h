@@ -1,0 +1,52 @@
+// gemm_instances.h -- instantiation table of marlin_gemm_kernel for one weight format.
+// Included by gemm_<fmt>.hip with MMI_FMT and MMI_FN defined, so the formats compile in
+// parallel translation units.
+#include "host_common.h"
+
+namespace mmi {
+
+template <int FMT, class AT, int GSM>
+static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
+  const dim3 grid(l.grid), block(256);
+#define MMI_CASE(BM_, NT_, MOE_)                                                               \
+  if (l.bm == BM_ && l.nt == NT_ && l.moe == MOE_) {                                           \
+    hipLaunchKernelGGL((marlin_gemm_kernel<FMT, AT, BM_, NT_, GSM, MOE_>), grid, block, 0, s, p); \
+    return hipGetLastError();                                                                  \
+  }
+  // dense
+  MMI_CASE(16, 1, false)
+  MMI_CASE(16, 2, false)
+  MMI_CASE(16, 4, false)
+  MMI_CASE(32, 2, false)
+  MMI_CASE(64, 4, false)
+  MMI_CASE(128, 4, false)
+  // MoE: one moe block per workgroup
+  MMI_CASE(16, 4, true)
+  MMI_CASE(32, 4, true)
+  MMI_CASE(48, 4, true)
+  MMI_CASE(64, 4, true)
+#undef MMI_CASE
+  return hipErrorInvalidValue;
+}
+
+template <int FMT, class AT>
+static hipError_t launch_at(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
+  if constexpr (FMT == FMT_MXFP4 || FMT == FMT_NVFP4) {
+    if (l.gsm == GSM_SMALL) return launch_gsm<FMT, AT, GSM_SMALL>(l, p, s);
+  } else if constexpr (FMT == FMT_FP8) {
+    if (l.gsm == GSM_CHANNEL) return launch_gsm<FMT, AT, GSM_CHANNEL>(l, p, s);
+    if (l.gsm == GSM_BIG) return launch_gsm<FMT, AT, GSM_BIG>(l, p, s);
+  } else {
+    if (l.gsm == GSM_CHANNEL) return launch_gsm<FMT, AT, GSM_CHANNEL>(l, p, s);
+    if (l.gsm == GSM_BIG) return launch_gsm<FMT, AT, GSM_BIG>(l, p, s);
+    if (l.gsm == GSM_SMALL) return launch_gsm<FMT, AT, GSM_SMALL>(l, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t MMI_FN(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
+  if (l.fmt != MMI_FMT) return hipErrorInvalidValue;
+  return l.bf16 ? launch_at<MMI_FMT, BF16>(l, p, s) : launch_at<MMI_FMT, F16>(l, p, s);
+}
+
+}  // namespace mmi

@@ -1,0 +1,418 @@
+// gemm_kernel.h -- gfx950 mixed-precision GEMM mainloop shared by the dense and MoE ops.
+//
+// Work decomposition (one workgroup = 4 wavefronts = 256 threads):
+//   * a workgroup owns a BM x BN output block, BN = 4 waves x NT n16-tiles x 16 columns;
+//     all four waves share the BM activation rows and own disjoint columns, so no weight
+//     is dequantized twice;
+//   * K advances in steps of 128.  Activation rows for the step are copied straight into LDS
+//     with global_load_lds_dwordx4 (no VGPR staging), laid out fragment-major so every
+//     ds_read_b128 of an MFMA A operand is conflict-free;
+//   * weights never touch LDS: each lane loads its dwordx4 of the tile-chunk layout
+//     (device_common.h), dequantizes in registers and feeds v_mfma_f32_16x16x32;
+//   * the next step's activations (LDS, double buffered), weights and scale metadata are
+//     in flight while the current step computes;
+//   * split-K partitions the K steps; partial sums go to an fp32 workspace with device-scope
+//     atomics, the last workgroup to finish an output block (per-block arrival counter)
+//     applies the epilogue and resets its workspace slice and counter to zero, so the
+//     workspace needs no clearing between calls.
+// MoE (reference sm70_marlin_gemm.cuh:3591-3686): a workgroup's rows are one moe block of
+// expert-sorted route ids; A rows are gathered as id / top_k, C rows scattered to id.
+#pragma once
+
+#include "device_common.h"
+
+namespace mmi {
+
+struct GemmParams {
+  const void* a;
+  int64_t a_stride;  // elements between rows of A
+  void* c;           // output rows of N elements
+  const uint32_t* b;
+  int64_t b_expert_stride;  // words per expert (MoE)
+  const void* scales;       // [E][G][N]
+  const void* zeros;        // [E][G][N] float zero points (same dtype as A) or null
+  int64_t meta_expert_stride;  // G*N
+  const void* bias;            // [E][N] permuted, or null
+  const float* global_scale;   // NVFP4: [E]
+  int alpha_exp;               // alpha = ldexp(global_scale[e], alpha_exp)
+  int M, N, K;
+  int group_shift;  // log2(group size) for grouped modes
+  int splits;
+  int steps_per_split;
+  int num_n_blocks;
+  float* ws;
+  int* counters;
+  // MoE
+  const int* sorted_ids;
+  int sorted_numel;
+  const int* expert_ids;
+  int expert_ids_numel;
+  const int* num_post_pad;
+  const float* topk_w;
+  int top_k;
+  int moe_bs;
+  int mul_topk;
+  int valid_ids;  // size_m * top_k
+};
+
+// Group-size modes.
+enum { GSM_CHANNEL = 0, GSM_BIG = 1, GSM_SMALL = 2 };
+
+template <class AT>
+__device__ __forceinline__ uint32_t load_u16(const void* p, int64_t idx) {
+  return (uint32_t)(reinterpret_cast<const uint16_t*>(p)[idx]);
+}
+
+template <int FMT, class AT>
+__device__ __forceinline__ uint32_t load_meta_raw(const GemmParams& p, int64_t base, int group,
+                                                  int col) {
+  const int64_t idx = base + (int64_t)group * p.N;
+  if constexpr (FMT == FMT_NVFP4) {
+    // NVFP4 scales are stored with a [0,2,1,3] shuffle per 4 columns
+    // (marlin_utils_fp4.py:83-86); the shuffle is its own inverse.
+    const int sc = (col & ~3) | ((col & 1) << 1) | ((col & 2) >> 1);
+    return reinterpret_cast<const uint8_t*>(p.scales)[idx + sc];
+  } else if constexpr (FMT == FMT_MXFP4) {
+    return reinterpret_cast<const uint8_t*>(p.scales)[idx + col];
+  } else if constexpr (fmt_has_zp(FMT)) {
+    return load_u16<AT>(p.scales, idx + col) | (load_u16<AT>(p.zeros, idx + col) << 16);
+  } else {
+    return load_u16<AT>(p.scales, idx + col);
+  }
+}
+
+__device__ __forceinline__ void lds_dma16(const void* gptr, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)lds_wave_base,
+                                   16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int FMT, class AT, int BM, int NT, int GSM, bool MOE>
+__global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
+  constexpr int MT = BM / 16;
+  constexpr int BITS = fmt_bits(FMT);
+  constexpr int BN = 4 * NT * 16;
+  constexpr int NW = (BITS == 4) ? 1 : 2;  // uint4 loads per tile per full step
+  constexpr int FRAGS = 4 * MT;            // A fragments per step
+  static_assert(FRAGS % 4 == 0, "fragments split evenly over 4 waves");
+
+  __shared__ u32x4_t lds_a[2][FRAGS * 64];
+  __shared__ int lds_rows[BM];
+  __shared__ int lds_last;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lg = lane >> 4;   // lane group: k-slice 8*lg inside a 32-deep block
+  const int ln = lane & 15;   // column (B) / row (A) inside a 16-wide fragment
+
+  int bid = blockIdx.x;
+  const int split = bid % p.splits;
+  bid /= p.splits;
+  const int n_blk = bid % p.num_n_blocks;
+  const int m_blk = bid / p.num_n_blocks;
+  const int out_tile = bid;
+
+  int expert = 0;
+  const AT* a = reinterpret_cast<const AT*>(p.a);
+  if constexpr (MOE) {
+    const int padded = p.num_post_pad[0];
+    if (m_blk * p.moe_bs >= padded || m_blk >= p.expert_ids_numel) return;
+    expert = p.expert_ids[m_blk];
+    if (expert < 0) return;
+    for (int r = tid; r < BM; r += 256) {
+      int id = -1;
+      const int si = m_blk * p.moe_bs + r;
+      if (r < p.moe_bs && si < p.sorted_numel && si < padded) {
+        id = p.sorted_ids[si];
+        if (id < 0 || id >= p.valid_ids) id = -1;
+      }
+      lds_rows[r] = id;
+    }
+    __syncthreads();
+  }
+  const int m0 = MOE ? 0 : m_blk * BM;
+
+  // ---- activation rows this wave copies into LDS: fragments f = wave + 4*i --------------
+  constexpr int FPW = FRAGS / 4;  // fragments per wave per step
+  const AT* a_src[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wave + 4 * i;
+    const int b = f / MT;
+    const int mt = f % MT;
+    const int r = mt * 16 + ln;
+    int64_t row;
+    if constexpr (MOE) {
+      const int id = lds_rows[r];
+      row = id >= 0 ? id / p.top_k : 0;
+    } else {
+      row = min(m0 + r, p.M - 1);
+    }
+    a_src[i] = a + row * p.a_stride + 32 * b + 8 * lg;
+  }
+
+  // ---- weight / metadata addressing ------------------------------------------------------
+  const int tn0 = n_blk * (BN / 16) + wave * NT;  // first n16 tile of this wave
+  const int64_t twords = tile_words(BITS, p.K);
+  const uint32_t* bptr = p.b + (int64_t)expert * p.b_expert_stride + (int64_t)tn0 * twords;
+  const int64_t meta_base = (int64_t)expert * p.meta_expert_stride;
+
+  const int total_full = p.K / 128;
+  const int k_tail = p.K - total_full * 128;
+  const int s_begin = split * p.steps_per_split;
+  const int s_end = min(total_full, s_begin + p.steps_per_split);
+  const bool do_tail = (k_tail != 0) && (split == p.splits - 1);
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Channelwise metadata is loop invariant.
+  Meta meta_ch[NT];
+  if constexpr (GSM == GSM_CHANNEL) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
+  }
+
+  constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
+  auto load_step = [&](int s, int buf, u32x4_t (&bw)[NT][NW], uint32_t (&raw)[NT][RAWB]) {
+    // activations -> LDS
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) {
+      const int f = wave + 4 * i;
+      lds_dma16(a_src[i] + s * 128, &lds_a[buf][f * 64]);
+    }
+    // weights
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint32_t* tp = bptr + t * twords + lane * 4;
+      if constexpr (BITS == 4) {
+        bw[t][0] = *reinterpret_cast<const u32x4_t*>(tp + (int64_t)s * 256);
+      } else {
+        bw[t][0] = *reinterpret_cast<const u32x4_t*>(tp + (int64_t)(2 * s) * 256);
+        bw[t][1] = *reinterpret_cast<const u32x4_t*>(tp + (int64_t)(2 * s + 1) * 256);
+      }
+    }
+    // metadata
+    if constexpr (GSM == GSM_BIG) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        raw[t][0] = load_meta_raw<FMT, AT>(p, meta_base, (s * 128) >> p.group_shift,
+                                           (tn0 + t) * 16 + ln);
+    } else if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          raw[t][b] = load_meta_raw<FMT, AT>(p, meta_base, (s * 128 + 32 * b + 8 * lg) >> p.group_shift,
+                                             (tn0 + t) * 16 + ln);
+    }
+  };
+
+  auto compute_block = [&](int buf, int b, const uint32_t w0[NT], const uint32_t w1[NT],
+                           const Meta (&mt_meta)[NT]) {
+    u32x4_t af[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af[i] = lds_a[buf][(b * MT + i) * 64 + lane];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4_t bop = dequant_operand<FMT, AT>(w0[t], w1[t], mt_meta[t]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i][t] = mfma16(af[i], bop, acc[i][t], AT{});
+    }
+  };
+
+  auto compute_step = [&](int buf, const u32x4_t (&bw)[NT][NW], const uint32_t (&raw)[NT][RAWB],
+                          int nblocks) {
+    Meta mm[NT];
+    if constexpr (GSM == GSM_CHANNEL) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) mm[t] = meta_ch[t];
+    } else if constexpr (GSM == GSM_BIG) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(raw[t][0]);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (b < nblocks) {
+        if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(raw[t][b]);
+        }
+        uint32_t w0[NT], w1[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if constexpr (BITS == 4) {
+            w0[t] = bw[t][0][b];
+            w1[t] = 0;
+          } else {
+            w0[t] = bw[t][b >> 1][(b & 1) * 2];
+            w1[t] = bw[t][b >> 1][(b & 1) * 2 + 1];
+          }
+        }
+        compute_block(buf, b, w0, w1, mm);
+      }
+    }
+  };
+
+  // ---- main loop over full 128-deep steps -------------------------------------------------
+  int buf = 0;
+  if (s_begin < s_end) {
+    u32x4_t bcur[NT][NW], bnext[NT][NW];
+    uint32_t rcur[NT][RAWB], rnext[NT][RAWB];
+    load_step(s_begin, 0, bcur, rcur);
+    wait_vm_all();
+    __syncthreads();
+    for (int s = s_begin; s < s_end; ++s) {
+      const bool more = s + 1 < s_end;
+      if (more) load_step(s + 1, buf ^ 1, bnext, rnext);
+      compute_step(buf, bcur, rcur, 4);
+      wait_vm_all();
+      __syncthreads();
+      if (more) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+          for (int w = 0; w < NW; ++w) bcur[t][w] = bnext[t][w];
+#pragma unroll
+          for (int r = 0; r < RAWB; ++r) rcur[t][r] = rnext[t][r];
+        }
+      }
+      buf ^= 1;
+    }
+  }
+
+  // ---- K tail: (K % 128) / 32 blocks, read word by word through the layout map -----------
+  if (do_tail) {
+    const int nblocks = k_tail / 32;
+    const int kt0 = total_full * 128;
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) {
+      const int f = wave + 4 * i;
+      const int b = f / MT;
+      if (b < nblocks) lds_dma16(a_src[i] + kt0, &lds_a[buf][f * 64]);
+    }
+    u32x4_t bw[NT][NW];
+    uint32_t raw[NT][RAWB];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t n = (int64_t)(tn0 + t) * 16 + ln;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          const int64_t k = kt0 + 32 * b + 8 * lg;
+          const uint32_t* base = p.b + (int64_t)expert * p.b_expert_stride;
+          if constexpr (BITS == 4) {
+            bw[t][0][b] = base[layout_word_index(4, p.K, n, k)];
+          } else {
+            bw[t][b >> 1][(b & 1) * 2] = base[layout_word_index(8, p.K, n, k)];
+            bw[t][b >> 1][(b & 1) * 2 + 1] = base[layout_word_index(8, p.K, n, k + 4)];
+          }
+        }
+      }
+      if constexpr (GSM == GSM_BIG) {
+        raw[t][0] = load_meta_raw<FMT, AT>(p, meta_base, kt0 >> p.group_shift, (int)n);
+      } else if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          raw[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, meta_base,
+                                                          (kt0 + 32 * b + 8 * lg) >> p.group_shift,
+                                                          (int)n)
+                                  : 0u;
+      }
+    }
+    wait_vm_all();
+    __syncthreads();
+    compute_step(buf, bw, raw, nblocks);
+  }
+
+  // ---- epilogue --------------------------------------------------------------------------
+  float alpha = 1.0f;
+  if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[expert], p.alpha_exp);
+  const AT* bias = reinterpret_cast<const AT*>(p.bias);
+  AT* cout = reinterpret_cast<AT*>(p.c);
+
+  auto out_row = [&](int r) -> int64_t {  // -1 when the row is not stored
+    if constexpr (MOE) {
+      return lds_rows[r];
+    } else {
+      return (m0 + r < p.M) ? (int64_t)(m0 + r) : -1;
+    }
+  };
+
+  auto finish = [&](int r, int col, float v) {
+    const int64_t orow = out_row(r);
+    if (orow < 0) return;
+    float o = v * alpha;
+    if (bias != nullptr) {
+      float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
+                                AT{});
+      if constexpr (MOE) {
+        if (p.mul_topk) bv *= alpha;
+      }
+      o += bv;
+    }
+    if constexpr (MOE) {
+      if (p.mul_topk) o *= p.topk_w[orow];
+    }
+    reinterpret_cast<uint16_t*>(cout)[orow * p.N + col] = to_raw16(o, AT{});
+  };
+
+  if (p.splits == 1) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          finish(i * 16 + lg * 4 + e, (tn0 + t) * 16 + ln, acc[i][t][e]);
+    return;
+  }
+
+  // split-K: accumulate into the fp32 workspace, last arriver finishes the block.
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t orow = out_row(i * 16 + lg * 4 + e);
+        if (orow >= 0)
+          __hip_atomic_fetch_add(p.ws + orow * p.N + (tn0 + t) * 16 + ln, acc[i][t][e],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(p.counters + out_tile, 1, __ATOMIC_ACQ_REL,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    lds_last = (prev == p.splits - 1);
+  }
+  __syncthreads();
+  if (!lds_last) return;
+  __threadfence();
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = i * 16 + lg * 4 + e;
+        const int64_t orow = out_row(r);
+        if (orow >= 0) {
+          const int col = (tn0 + t) * 16 + ln;
+          const float v = __hip_atomic_exchange(p.ws + orow * p.N + col, 0.0f, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+          finish(r, col, v);
+        }
+      }
+  if (tid == 0)
+    __hip_atomic_store(p.counters + out_tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace mmi

@@ -1,0 +1,46 @@
+// host_common.h -- host-side declarations shared by the launch and C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "gemm_kernel.h"
+
+namespace mmi {
+
+// Launchers (defined in the .hip files).
+hipError_t launch_gptq_repack(const uint32_t* src, const int* perm, uint32_t* out, int64_t size_k,
+                              int64_t size_n, int bits, hipStream_t stream);
+hipError_t launch_awq_repack(const uint32_t* src, uint32_t* out, int64_t size_k, int64_t size_n,
+                             int bits, hipStream_t stream);
+hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, int gs_mode,
+                          hipStream_t stream);
+hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, int bs, int* sorted,
+                            int64_t sorted_numel, int* expert_ids, int64_t expert_ids_numel,
+                            int* post_pad, const int* expert_map, hipStream_t stream);
+hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, int64_t hidden,
+                          void* out, hipStream_t stream);
+
+// One GEMM launch configuration.
+struct GemmLaunch {
+  int fmt;
+  bool bf16;
+  int gsm;   // GSM_CHANNEL / GSM_BIG / GSM_SMALL
+  int bm;    // rows per workgroup
+  int nt;    // n16 tiles per wave
+  bool moe;
+  unsigned grid;
+};
+// Defined per format in gemm_<fmt>.hip; returns hipErrorInvalidValue for a configuration
+// that is not instantiated.
+hipError_t launch_gemm_u4b8(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm_u4(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm_u8b128(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm_u8(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm_fp8(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm_mxfp4(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm_nvfp4(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+
+}  // namespace mmi

@@ -1,0 +1,433 @@
+// torch_ops.cpp -- thin TORCH_LIBRARY binding of the reference op schemas over the C ABI.
+//
+// Built twice: with MMI_EXT_NAME=_C it registers torch.ops._C.{marlin_gemm,
+// gptq_marlin_repack, awq_marlin_repack} (schemas byte-identical to the reference
+// csrc/torch_bindings_marlin.cpp:6-21); with MMI_EXT_NAME=_moe_C it registers
+// torch.ops._moe_C.{moe_align_block_size, moe_wna16_marlin_gemm, moe_sum}
+// (csrc/moe/torch_bindings_marlin.cpp:17-47).  The _C build also registers the inspection op
+// torch.ops._marlin_mi355x.dequantize.  Tensor-level checks (device, contiguity, ranks,
+// shapes) mirror the reference's TORCH_CHECKs; everything else is validated by the C ABI,
+// whose messages are rethrown unchanged.
+#include <Python.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/all.h>
+#include <torch/library.h>
+
+#include "../../include/marlin_mi355x.h"
+
+#ifndef MMI_EXT_NAME
+#error "MMI_EXT_NAME must be _C or _moe_C"
+#endif
+#define MMI_STR2(x) #x
+#define MMI_STR(x) MMI_STR2(x)
+
+namespace {
+
+marlin_dtype_t to_mdt(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf: return MARLIN_DTYPE_FLOAT16;
+    case at::kBFloat16: return MARLIN_DTYPE_BFLOAT16;
+    case at::kFloat: return MARLIN_DTYPE_FLOAT32;
+    case at::kFloat8_e4m3fn: return MARLIN_DTYPE_FLOAT8_E4M3FN;
+    case at::kFloat8_e8m0fnu: return MARLIN_DTYPE_FLOAT8_E8M0FNU;
+    case at::kInt: return MARLIN_DTYPE_INT32;
+    case at::kLong: return MARLIN_DTYPE_INT64;
+    case at::kByte: return MARLIN_DTYPE_UINT8;
+    case at::kChar: return MARLIN_DTYPE_INT8;
+    default: return (marlin_dtype_t)-1;
+  }
+}
+
+marlin_stream_t cur_stream(const at::Tensor& t) {
+  return reinterpret_cast<marlin_stream_t>(
+      c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void rethrow(marlin_status_t st) {
+  TORCH_CHECK(st == MARLIN_STATUS_OK, marlin_get_last_error());
+}
+
+const void* opt_ptr(const std::optional<at::Tensor>& t) {
+  return (t.has_value() && t->numel() > 0) ? t->data_ptr() : nullptr;
+}
+int64_t opt_numel(const std::optional<at::Tensor>& t) { return t.has_value() ? t->numel() : 0; }
+marlin_dtype_t opt_dtype(const std::optional<at::Tensor>& t) {
+  return t.has_value() ? to_mdt(t->scalar_type()) : MARLIN_DTYPE_FLOAT16;
+}
+
+void check_cuda_contig(const std::optional<at::Tensor>& t, const char* name) {
+  if (!t.has_value()) return;
+  TORCH_CHECK(t->device().is_cuda(), name, " is not on GPU");
+  TORCH_CHECK(t->is_contiguous(), name, " is not contiguous");
+}
+
+}  // namespace
+
+#if defined(MMI_BUILD_C)
+
+// reference gptq_marlin_repack.cu:399-469
+at::Tensor op_gptq_marlin_repack(at::Tensor& b_q_weight, at::Tensor& perm, int64_t size_k,
+                              int64_t size_n, int64_t num_bits, bool is_a_8bit) {
+  TORCH_CHECK(num_bits == 4 || num_bits == 8, "num_bits must be 4 or 8. Got = ", num_bits);
+  const int64_t pack = 32 / num_bits;
+  TORCH_CHECK((size_k / pack) == b_q_weight.size(0), "Shape mismatch: b_q_weight.size(0) = ",
+              b_q_weight.size(0), ", size_k = ", size_k, ", pack_factor = ", pack);
+  TORCH_CHECK(b_q_weight.size(1) == size_n, "b_q_weight.size(1) = ", b_q_weight.size(1),
+              " is not size_n = ", size_n);
+  TORCH_CHECK(b_q_weight.device().is_cuda(), "b_q_weight is not on GPU");
+  TORCH_CHECK(b_q_weight.is_contiguous(), "b_q_weight is not contiguous");
+  TORCH_CHECK(b_q_weight.dtype() == at::kInt, "b_q_weight type is not kInt");
+  TORCH_CHECK(perm.device().is_cuda(), "perm is not on GPU");
+  TORCH_CHECK(perm.is_contiguous(), "perm is not contiguous");
+  TORCH_CHECK(perm.dtype() == at::kInt, "perm type is not at::kInt");
+  const c10::hip::OptionalHIPGuard guard(b_q_weight.device());
+  at::Tensor out = torch::empty({size_k / 16, size_n * 16 / pack}, b_q_weight.options());
+  rethrow(marlin_gptq_marlin_repack(b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(),
+                                    perm.numel() ? perm.data_ptr<int32_t>() : nullptr,
+                                    perm.numel(), size_k, size_n, num_bits, is_a_8bit,
+                                    out.data_ptr<int32_t>(), out.numel(), cur_stream(b_q_weight)));
+  return out;
+}
+
+// reference awq_marlin_repack.cu:300-381
+at::Tensor op_awq_marlin_repack(at::Tensor& b_q_weight, int64_t size_k, int64_t size_n,
+                             int64_t num_bits, bool is_a_8bit) {
+  TORCH_CHECK(num_bits == 4 || num_bits == 8, "num_bits must be 4 or 8. Got = ", num_bits);
+  const int64_t pack = 32 / num_bits;
+  TORCH_CHECK(b_q_weight.size(0) == size_k, "b_q_weight.size(0) = ", b_q_weight.size(0),
+              " is not size_k = ", size_k);
+  TORCH_CHECK((size_n / pack) == b_q_weight.size(1), "Shape mismatch: b_q_weight.size(1) = ",
+              b_q_weight.size(1), ", size_n = ", size_n, ", pack_factor = ", pack);
+  TORCH_CHECK(b_q_weight.device().is_cuda(), "b_q_weight is not on GPU");
+  TORCH_CHECK(b_q_weight.is_contiguous(), "b_q_weight is not contiguous");
+  TORCH_CHECK(b_q_weight.dtype() == at::kInt, "b_q_weight type is not kInt");
+  const c10::hip::OptionalHIPGuard guard(b_q_weight.device());
+  at::Tensor out = torch::empty({size_k / 16, size_n * 16 / pack}, b_q_weight.options());
+  rethrow(marlin_awq_marlin_repack(b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(), size_k,
+                                   size_n, num_bits, is_a_8bit, out.data_ptr<int32_t>(),
+                                   out.numel(), cur_stream(b_q_weight)));
+  return out;
+}
+
+// reference marlin.cu:83-506
+at::Tensor op_marlin_gemm(at::Tensor& a, std::optional<at::Tensor> c_or_none, at::Tensor& b_q_weight,
+                       std::optional<at::Tensor> const& b_bias_or_none, at::Tensor& b_scales,
+                       std::optional<at::Tensor> const& a_scales_or_none,
+                       std::optional<at::Tensor> const& global_scale_or_none,
+                       std::optional<at::Tensor> const& b_zeros_or_none,
+                       std::optional<at::Tensor> const& g_idx_or_none,
+                       std::optional<at::Tensor> const& perm_or_none, at::Tensor& workspace,
+                       int64_t b_type_id, int64_t size_m, int64_t size_n, int64_t size_k,
+                       bool is_k_full, bool use_atomic_add, bool use_fp32_reduce,
+                       bool is_zp_float) {
+  TORCH_CHECK(a.scalar_type() == at::kHalf || a.scalar_type() == at::kBFloat16,
+              "only float16 and bfloat16 activations are supported (8-bit activations are not "
+              "implemented).");
+  TORCH_CHECK(a.size(0) == size_m, "Shape mismatch: a.size(0) = ", a.size(0), ", size_m = ",
+              size_m);
+  TORCH_CHECK(a.size(1) == size_k, "Shape mismatch: a.size(1) = ", a.size(1), ", size_k = ",
+              size_k);
+  TORCH_CHECK(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
+  TORCH_CHECK(b_q_weight.dim() == 2, "b_q_weight rank must be 2");
+  TORCH_CHECK((size_k / 16) == b_q_weight.size(0), "Shape mismatch: b_q_weight.size(0) = ",
+              b_q_weight.size(0), ", size_k = ", size_k, ", tile_size = ", 16);
+  TORCH_CHECK(b_q_weight.size(1) % 16 == 0, "b_q_weight.size(1) = ", b_q_weight.size(1),
+              " is not divisible by tile_size = ", 16);
+  TORCH_CHECK(a.device().is_cuda(), "A is not on GPU");
+  TORCH_CHECK(a.stride(1) == 1, "A.stride(1) is not 1");
+  TORCH_CHECK(b_q_weight.device().is_cuda(), "b_q_weight is not on GPU");
+  TORCH_CHECK(b_q_weight.is_contiguous(), "b_q_weight is not contiguous");
+  TORCH_CHECK(b_q_weight.scalar_type() == at::kInt, "expects int32 packed weights.");
+  TORCH_CHECK(b_scales.device().is_cuda(), "b_scales is not on GPU");
+  TORCH_CHECK(b_scales.is_contiguous(), "b_scales is not contiguous");
+  TORCH_CHECK(b_scales.dim() == 2, "b_scales rank = ", b_scales.dim(), " is not 2");
+  TORCH_CHECK(b_scales.size(1) == size_n, "b_scales dim 1 = ", b_scales.size(1),
+              " is not size_n = ", size_n);
+  check_cuda_contig(global_scale_or_none, "global_scale");
+  check_cuda_contig(b_bias_or_none, "b_bias");
+  check_cuda_contig(b_zeros_or_none, "b_zeros");
+  if (global_scale_or_none.has_value())
+    TORCH_CHECK(global_scale_or_none->scalar_type() == at::kFloat,
+                "nvfp4 expects fp32 global_scale.");
+  if (b_bias_or_none.has_value()) {
+    TORCH_CHECK(b_bias_or_none->scalar_type() == a.scalar_type(),
+                "b_bias must have the activation dtype.");
+    TORCH_CHECK(b_bias_or_none->size(0) == size_n, "b_bias.size(0) != size_n");
+  }
+  if (b_zeros_or_none.has_value() && b_zeros_or_none->size(-1) > 0) {
+    TORCH_CHECK(b_zeros_or_none->dim() == 2, "b_zeros rank = ", b_zeros_or_none->dim(),
+                " is not 2");
+    TORCH_CHECK(b_zeros_or_none->size(1) == size_n, "b_zeros dim 1 = ",
+                b_zeros_or_none->size(1), " is not size_n = ", size_n);
+    TORCH_CHECK(b_zeros_or_none->size(0) == b_scales.size(0), "b_zeros dim 0 = ",
+                b_zeros_or_none->size(0), " is not num_groups = ", b_scales.size(0));
+  }
+
+  const c10::hip::OptionalHIPGuard guard(a.device());
+  at::Tensor c;
+  if (c_or_none.has_value()) {
+    c = c_or_none.value();
+    TORCH_CHECK(c.device().is_cuda(), "c is not on GPU");
+    TORCH_CHECK(c.is_contiguous(), "c is not contiguous");
+    TORCH_CHECK(c.scalar_type() == a.scalar_type(),
+                "scalar type of a must be the same with c for 16 bit activation");
+    TORCH_CHECK(c.size(0) == size_m, "Shape mismatch: c.size(0) = ", c.size(0), ", size_m = ",
+                size_m);
+    TORCH_CHECK(c.size(1) == size_n, "Shape mismatch: c.size(1) = ", c.size(1), ", size_n = ",
+                size_n);
+  } else {
+    c = torch::empty({size_m, size_n}, a.options());
+  }
+  if (size_m == 0) return c;
+
+  const int64_t zeros_numel =
+      (b_zeros_or_none.has_value() && b_zeros_or_none->size(-1) > 0) ? b_zeros_or_none->numel() : 0;
+  rethrow(marlin_gemm(a.data_ptr(), to_mdt(a.scalar_type()), a.stride(0), c.data_ptr(),
+                      b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(), opt_ptr(b_bias_or_none),
+                      opt_numel(b_bias_or_none), b_scales.data_ptr(),
+                      to_mdt(b_scales.scalar_type()), b_scales.numel(), b_scales.size(0),
+                      opt_numel(a_scales_or_none),
+                      reinterpret_cast<const float*>(opt_ptr(global_scale_or_none)),
+                      opt_numel(global_scale_or_none), opt_ptr(b_zeros_or_none),
+                      opt_dtype(b_zeros_or_none), zeros_numel, opt_numel(g_idx_or_none),
+                      opt_numel(perm_or_none), workspace.numel() ? workspace.data_ptr() : nullptr,
+                      workspace.nbytes(), b_type_id, size_m, size_n, size_k, is_k_full,
+                      use_atomic_add, use_fp32_reduce, is_zp_float, cur_stream(a)));
+  return c;
+}
+
+// Inspection op: dequantize repacked weights with the GEMM's device routines.
+at::Tensor mmi_dequantize(at::Tensor& b_q_weight, at::Tensor& b_scales,
+                          std::optional<at::Tensor> const& b_zeros_or_none,
+                          std::optional<at::Tensor> const& global_scale_or_none,
+                          int64_t b_type_id, int64_t size_k, int64_t size_n,
+                          at::ScalarType out_dtype) {
+  TORCH_CHECK(b_q_weight.is_cuda() && b_q_weight.is_contiguous(), "b_q_weight");
+  TORCH_CHECK(b_scales.is_cuda() && b_scales.is_contiguous() && b_scales.dim() == 2 &&
+                  b_scales.size(1) == size_n,
+              "b_scales must be a contiguous [num_groups, size_n] GPU tensor");
+  check_cuda_contig(b_zeros_or_none, "b_zeros");
+  check_cuda_contig(global_scale_or_none, "global_scale");
+  const c10::hip::OptionalHIPGuard guard(b_q_weight.device());
+  at::Tensor out = torch::empty({size_k, size_n}, b_q_weight.options().dtype(out_dtype));
+  rethrow(marlin_dequantize(b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(),
+                            b_scales.data_ptr(), to_mdt(b_scales.scalar_type()), b_scales.numel(),
+                            b_scales.size(0), opt_ptr(b_zeros_or_none), opt_dtype(b_zeros_or_none),
+                            opt_numel(b_zeros_or_none),
+                            reinterpret_cast<const float*>(opt_ptr(global_scale_or_none)),
+                            opt_numel(global_scale_or_none), b_type_id, size_k, size_n,
+                            to_mdt(out_dtype), out.data_ptr(), cur_stream(b_q_weight)));
+  return out;
+}
+
+TORCH_LIBRARY(_C, ops) {
+  ops.def(
+      "marlin_gemm(Tensor a, Tensor? c_or_none, Tensor b_q_weight, "
+      "Tensor? b_bias_or_none,Tensor b_scales, "
+      "Tensor? a_scales, Tensor? global_scale, Tensor? b_zeros_or_none, "
+      "Tensor? g_idx_or_none, Tensor? perm_or_none, Tensor workspace, "
+      "int b_type_id, SymInt size_m, SymInt size_n, SymInt size_k, "
+      "bool is_k_full, bool use_atomic_add, bool use_fp32_reduce, "
+      "bool is_zp_float) -> Tensor");
+  ops.def(
+      "gptq_marlin_repack(Tensor b_q_weight, Tensor perm, "
+      "SymInt size_k, SymInt size_n, int num_bits, bool is_a_8bit) -> Tensor");
+  ops.def(
+      "awq_marlin_repack(Tensor b_q_weight, SymInt size_k, "
+      "SymInt size_n, int num_bits, bool is_a_8bit) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(_C, CUDA, ops) {
+  ops.impl("marlin_gemm", &op_marlin_gemm);
+  ops.impl("gptq_marlin_repack", &op_gptq_marlin_repack);
+  ops.impl("awq_marlin_repack", &op_awq_marlin_repack);
+}
+
+TORCH_LIBRARY(_marlin_mi355x, ops) {
+  ops.def(
+      "dequantize(Tensor b_q_weight, Tensor b_scales, Tensor? b_zeros, Tensor? global_scale, "
+      "int b_type_id, SymInt size_k, SymInt size_n, ScalarType out_dtype) -> Tensor");
+}
+TORCH_LIBRARY_IMPL(_marlin_mi355x, CUDA, ops) { ops.impl("dequantize", &mmi_dequantize); }
+
+#elif defined(MMI_BUILD_MOE_C)
+
+// reference moe_align_sum_kernels.cu:477-569
+void op_moe_align_block_size(at::Tensor topk_ids, int64_t num_experts, int64_t block_size,
+                          at::Tensor sorted_token_ids, at::Tensor experts_ids,
+                          at::Tensor num_tokens_post_pad,
+                          std::optional<at::Tensor> maybe_expert_map) {
+  TORCH_CHECK(topk_ids.is_cuda() && topk_ids.is_contiguous(), "topk_ids must be a contiguous GPU tensor");
+  TORCH_CHECK(topk_ids.scalar_type() == at::kInt || topk_ids.scalar_type() == at::kLong,
+              "topk_ids must be int32 or int64");
+  for (const at::Tensor* t : {&sorted_token_ids, &experts_ids, &num_tokens_post_pad}) {
+    TORCH_CHECK(t->is_cuda() && t->is_contiguous() && t->scalar_type() == at::kInt,
+                "moe_align_block_size outputs must be contiguous int32 GPU tensors");
+  }
+  if (maybe_expert_map.has_value()) {
+    TORCH_CHECK(maybe_expert_map->is_cuda() && maybe_expert_map->is_contiguous() &&
+                    maybe_expert_map->scalar_type() == at::kInt,
+                "expert_map must be a contiguous int32 GPU tensor");
+  }
+  const c10::hip::OptionalHIPGuard guard(topk_ids.device());
+  rethrow(marlin_moe_align_block_size(
+      topk_ids.data_ptr(), to_mdt(topk_ids.scalar_type()), topk_ids.numel(), num_experts,
+      block_size, sorted_token_ids.data_ptr<int32_t>(), sorted_token_ids.numel(),
+      experts_ids.data_ptr<int32_t>(), experts_ids.numel(), num_tokens_post_pad.data_ptr<int32_t>(),
+      maybe_expert_map.has_value() ? maybe_expert_map->data_ptr<int32_t>() : nullptr,
+      opt_numel(maybe_expert_map), cur_stream(topk_ids)));
+}
+
+// reference csrc/moe/marlin_moe_wna16/ops.cu:102-529
+at::Tensor op_moe_wna16_marlin_gemm(
+    at::Tensor& a, std::optional<at::Tensor> c_or_none, at::Tensor& b_q_weight,
+    std::optional<at::Tensor> const& b_bias_or_none, at::Tensor& b_scales,
+    std::optional<at::Tensor> const& a_scales_or_none,
+    std::optional<at::Tensor> const& global_scale_or_none,
+    std::optional<at::Tensor> const& b_zeros_or_none,
+    std::optional<at::Tensor> const& g_idx_or_none, std::optional<at::Tensor> const& perm_or_none,
+    at::Tensor& workspace, at::Tensor& sorted_token_ids, at::Tensor& expert_ids,
+    at::Tensor& num_tokens_past_padded, at::Tensor& topk_weights, int64_t moe_block_size,
+    int64_t top_k, bool mul_topk_weights, int64_t b_type_id, int64_t size_m, int64_t size_n,
+    int64_t size_k, bool is_k_full, bool use_atomic_add, bool use_fp32_reduce, bool is_zp_float,
+    int64_t thread_k, int64_t thread_n, int64_t blocks_per_sm) {
+  TORCH_CHECK(a.scalar_type() == at::kHalf || a.scalar_type() == at::kBFloat16,
+              "only float16 and bfloat16 activations are supported (8-bit activations are not "
+              "implemented).");
+  TORCH_CHECK(a.size(0) == size_m, "Shape mismatch: a.size(0) = ", a.size(0), ", size_m = ",
+              size_m);
+  TORCH_CHECK(a.size(1) == size_k, "Shape mismatch: a.size(1) = ", a.size(1), ", size_k = ",
+              size_k);
+  TORCH_CHECK(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
+  TORCH_CHECK(b_q_weight.dim() == 3, "b_q_weight rank must be 3");
+  TORCH_CHECK((size_k / 16) == b_q_weight.size(1), "Shape mismatch: b_q_weight.size(1) = ",
+              b_q_weight.size(1), ", size_k = ", size_k, ", tile_size = ", 16);
+  TORCH_CHECK(b_q_weight.size(2) % 16 == 0, "b_q_weight.size(2) = ", b_q_weight.size(2),
+              " is not divisible by tile_size = ", 16);
+  TORCH_CHECK(a.device().is_cuda(), "A is not on GPU");
+  TORCH_CHECK(a.is_contiguous(), "A is not contiguous");
+  TORCH_CHECK(b_q_weight.device().is_cuda(), "b_q_weight is not on GPU");
+  TORCH_CHECK(b_q_weight.is_contiguous(), "b_q_weight is not contiguous");
+  TORCH_CHECK(b_q_weight.scalar_type() == at::kInt, "expects int32 packed weights.");
+  TORCH_CHECK(b_scales.device().is_cuda(), "b_scales is not on GPU");
+  TORCH_CHECK(b_scales.is_contiguous(), "b_scales is not contiguous");
+  TORCH_CHECK(b_scales.dim() == 3, "b_scales rank = ", b_scales.dim(), " is not 3");
+  TORCH_CHECK(b_scales.size(2) == size_n, "b_scales dim 2 = ", b_scales.size(2),
+              " is not size_n = ", size_n);
+  const int64_t num_experts = b_q_weight.size(0);
+  check_cuda_contig(global_scale_or_none, "global_scale");
+  check_cuda_contig(b_bias_or_none, "b_bias");
+  check_cuda_contig(b_zeros_or_none, "b_zeros");
+  if (global_scale_or_none.has_value())
+    TORCH_CHECK(global_scale_or_none->scalar_type() == at::kFloat,
+                "nvfp4 expects fp32 global_scale.");
+  if (b_bias_or_none.has_value()) {
+    TORCH_CHECK(b_bias_or_none->scalar_type() == a.scalar_type(),
+                "b_bias must have the activation dtype.");
+    TORCH_CHECK(b_bias_or_none->size(0) == num_experts, "b_bias.size(0) != num_experts");
+    TORCH_CHECK(b_bias_or_none->size(1) == size_n, "b_bias.size(1) != size_n");
+  }
+  if (b_zeros_or_none.has_value() && b_zeros_or_none->size(-1) > 0) {
+    TORCH_CHECK(b_zeros_or_none->dim() == 3, "b_zeros rank = ", b_zeros_or_none->dim(),
+                " is not 3");
+    TORCH_CHECK(b_zeros_or_none->size(0) == num_experts, "b_zeros dim 0 = ",
+                b_zeros_or_none->size(0), " is not num_experts = ", num_experts);
+    TORCH_CHECK(b_zeros_or_none->size(1) == b_scales.size(1), "b_zeros dim 1 = ",
+                b_zeros_or_none->size(1), " is not num_groups = ", b_scales.size(1));
+    TORCH_CHECK(b_zeros_or_none->size(2) == size_n, "b_zeros dim 2 = ", b_zeros_or_none->size(2),
+                " is not size_n = ", size_n);
+  }
+  for (const at::Tensor* t : {&sorted_token_ids, &expert_ids, &num_tokens_past_padded}) {
+    TORCH_CHECK(t->is_cuda() && t->is_contiguous() && t->scalar_type() == at::kInt,
+                "sorted_token_ids / expert_ids / num_tokens_past_padded must be contiguous "
+                "int32 GPU tensors");
+  }
+  TORCH_CHECK(topk_weights.is_cuda() && topk_weights.is_contiguous() &&
+                  topk_weights.scalar_type() == at::kFloat,
+              "topk_weights must be a contiguous float32 GPU tensor");
+
+  const c10::hip::OptionalHIPGuard guard(a.device());
+  at::Tensor c;
+  if (c_or_none.has_value()) {
+    c = c_or_none.value();
+    TORCH_CHECK(c.device().is_cuda(), "c is not on GPU");
+    TORCH_CHECK(c.is_contiguous(), "c is not contiguous");
+    TORCH_CHECK(c.size(0) == size_m * top_k, "Shape mismatch: c.size(0) = ", c.size(0),
+                ", size_m * topk = ", size_m * top_k);
+    TORCH_CHECK(c.size(1) == size_n, "Shape mismatch: c.size(1) = ", c.size(1), ", size_n = ",
+                size_n);
+    TORCH_CHECK(c.scalar_type() == a.scalar_type(),
+                "scalar type of a must be the same with c for 16 bit activation");
+  } else {
+    c = torch::empty({size_m * top_k, size_n}, a.options());
+  }
+  const int64_t zeros_numel =
+      (b_zeros_or_none.has_value() && b_zeros_or_none->size(-1) > 0) ? b_zeros_or_none->numel() : 0;
+  rethrow(marlin_moe_wna16_marlin_gemm(
+      a.data_ptr(), to_mdt(a.scalar_type()), c.data_ptr(), b_q_weight.data_ptr<int32_t>(),
+      b_q_weight.numel(), num_experts, opt_ptr(b_bias_or_none), opt_numel(b_bias_or_none),
+      b_scales.data_ptr(), to_mdt(b_scales.scalar_type()), b_scales.numel(), b_scales.size(1),
+      opt_numel(a_scales_or_none), reinterpret_cast<const float*>(opt_ptr(global_scale_or_none)),
+      opt_numel(global_scale_or_none), opt_ptr(b_zeros_or_none), opt_dtype(b_zeros_or_none),
+      zeros_numel, opt_numel(g_idx_or_none), opt_numel(perm_or_none),
+      workspace.numel() ? workspace.data_ptr() : nullptr, workspace.nbytes(),
+      sorted_token_ids.data_ptr<int32_t>(), sorted_token_ids.numel(), expert_ids.data_ptr<int32_t>(),
+      expert_ids.numel(), num_tokens_past_padded.data_ptr<int32_t>(), topk_weights.data_ptr<float>(),
+      topk_weights.numel(), moe_block_size, top_k, mul_topk_weights, b_type_id, size_m, size_n,
+      size_k, is_k_full, use_atomic_add, use_fp32_reduce, is_zp_float, thread_k, thread_n,
+      blocks_per_sm, cur_stream(a)));
+  return c;
+}
+
+// upstream vLLM moe_sum: output[t, :] = sum over top_k of input[t, k, :]
+void op_moe_sum(at::Tensor& input, at::Tensor& output) {
+  TORCH_CHECK(input.is_cuda() && input.is_contiguous() && input.dim() == 3,
+              "input must be a contiguous [tokens, topk, hidden] GPU tensor");
+  TORCH_CHECK(output.is_cuda() && output.is_contiguous() && output.dim() == 2,
+              "output must be a contiguous [tokens, hidden] GPU tensor");
+  TORCH_CHECK(output.scalar_type() == input.scalar_type(), "dtype mismatch");
+  TORCH_CHECK(output.size(0) == input.size(0) && output.size(1) == input.size(2), "shape mismatch");
+  const c10::hip::OptionalHIPGuard guard(input.device());
+  rethrow(marlin_moe_sum(input.data_ptr(), to_mdt(input.scalar_type()), input.size(0),
+                         input.size(1), input.size(2), output.data_ptr(), cur_stream(input)));
+}
+
+TORCH_LIBRARY(_moe_C, m) {
+  m.def(
+      "moe_align_block_size(Tensor topk_ids, int num_experts,"
+      "                     int block_size, Tensor! sorted_token_ids,"
+      "                     Tensor! experts_ids,"
+      "                     Tensor! num_tokens_post_pad,"
+      "                     Tensor? maybe_expert_map) -> ()");
+  m.impl("moe_align_block_size", torch::kCUDA, &op_moe_align_block_size);
+  m.def(
+      "moe_wna16_marlin_gemm(Tensor! a, Tensor? c_or_none,"
+      "Tensor! b_q_weight, Tensor? b_bias_or_none,"
+      "Tensor! b_scales, Tensor? a_scales, Tensor? global_scale, Tensor? "
+      "b_zeros_or_none,"
+      "Tensor? g_idx_or_none, Tensor? perm_or_none, Tensor! workspace,"
+      "Tensor sorted_token_ids,"
+      "Tensor! expert_ids, Tensor! num_tokens_past_padded,"
+      "Tensor! topk_weights, int moe_block_size, int top_k, "
+      "bool mul_topk_weights, int b_type_id,"
+      "int size_m, int size_n, int size_k,"
+      "bool is_k_full, bool use_atomic_add,"
+      "bool use_fp32_reduce, bool is_zp_float,"
+      "int thread_k, int thread_n, int blocks_per_sm) -> Tensor");
+  m.impl("moe_wna16_marlin_gemm", torch::kCUDA, &op_moe_wna16_marlin_gemm);
+  m.def("moe_sum(Tensor input, Tensor! output) -> ()");
+  m.impl("moe_sum", torch::kCUDA, &op_moe_sum);
+}
+
+#endif
+
+// `import marlin_v100_amd._C` / `._moe_C` runs the static registrars above
+// (reference csrc/core/registration.h:22-27).
+#define MMI_CONCAT2(a, b) a##b
+#define MMI_CONCAT(a, b) MMI_CONCAT2(a, b)
+PyMODINIT_FUNC MMI_CONCAT(PyInit_, MMI_EXT_NAME)() {
+  static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, MMI_STR(MMI_EXT_NAME), nullptr, 0,
+                                      nullptr};
+  return PyModule_Create(&module);
+}

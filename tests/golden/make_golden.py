@@ -1,0 +1,47 @@
+"""Writes the golden fixtures restated from the reference's own tests (no reference code is
+imported or executed): the values below are copied from the cited test assertions.
+
+  scalar_type_ids.json : tests/test_marlin_helpers.py:69-86 and the ScalarType table of
+                         vllm/scalar_type.py:83-90 (ids as listed for the op ABI)
+  moe_align_kat.json   : tests/test_marlin_moe.py:274-291 (_moe_align_block_size_reference)
+  bias_perm.json       : csrc/quantization/marlin/sm70_marlin_bias.cuh:20-23
+"""
+import json
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+FIXTURES = {
+    "scalar_type_ids.json": {
+        "source": "tests/test_marlin_helpers.py:69-86; vllm/scalar_type.py:25-43,83-90",
+        "ids": {
+            "uint4": 1125899906843648,
+            "uint4b8": 1125899907892224,
+            "uint8": 1125899906844672,
+            "uint8b128": 1125899923621888,
+            "float4_e2m1f": (2 << 0) | (1 << 8) | (1 << 16) | (1 << 49),
+            "float8_e4m3fn": (4 << 0) | (3 << 8) | (1 << 16) | (1 << 49) | (2 << 50),
+            "float8_e8m0fnu": (8 << 0) | (1 << 49) | (2 << 50),
+        },
+    },
+    "moe_align_kat.json": {
+        "source": "tests/test_marlin_moe.py:274-291",
+        "topk_ids": [[0, 3], [1, 3], [0, 2], [1, 0]],
+        "num_experts": 4,
+        "block_size": 4,
+        "sorted_ids": [0, 4, 7, 8, 2, 6, 8, 8, 5, 8, 8, 8, 1, 3, 8, 8],
+        "expert_ids": [0, 1, 2, 3],
+        "num_tokens_post_pad": 16,
+    },
+    "bias_perm.json": {
+        "source": "csrc/quantization/marlin/sm70_marlin_bias.cuh:20-23",
+        "inverse_scale_perm_single": [0, 1, 8, 9, 16, 17, 24, 25, 2, 3, 10, 11, 18, 19, 26, 27,
+                                      4, 5, 12, 13, 20, 21, 28, 29, 6, 7, 14, 15, 22, 23, 30, 31],
+    },
+}
+
+if __name__ == "__main__":
+    for name, data in FIXTURES.items():
+        with open(os.path.join(HERE, name), "w") as f:
+            json.dump(data, f, indent=1)
+        print("wrote", name)

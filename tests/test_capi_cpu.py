@@ -1,0 +1,131 @@
+"""CPU checks of the C ABI: the library loads, exports every function include/*.h declares,
+and rejects invalid arguments before touching a GPU (the reference's TORCH_CHECK
+contract, csrc/quantization/marlin/marlin.cu:95-383, csrc/moe/marlin_moe_wna16/ops.cu:118-402)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from marlin_v100_amd import capi
+from tests.quant_cases import TYPE_ID
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for f in os.listdir(inc):
+        if f.endswith(".h"):
+            text = open(os.path.join(inc, f)).read()
+            names |= set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(marlin_\w+)\s*\(", text, re.M))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(capi.LIB_PATH)
+    declared = _declared_symbols()
+    assert {"marlin_gemm", "marlin_moe_wna16_marlin_gemm", "marlin_moe_align_block_size",
+            "marlin_gptq_marlin_repack", "marlin_awq_marlin_repack"} <= declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(capi.SIGNATURES) == declared
+
+
+def test_abi_version():
+    assert capi.load().marlin_abi_version() == 1
+
+
+def _gemm(**kw):
+    args = dict(a=16, a_dtype=capi.F16, a_row_stride=256, c=16, bq=16, bq_numel=256 * 512 // 8,
+                bias=None, bias_numel=0, scales=16, scales_dtype=capi.F16, scales_numel=2 * 512,
+                groups=2, a_scales_numel=0, glob=None, glob_numel=0, zeros=None,
+                zeros_dtype=capi.F16, zeros_numel=0, gidx=0, perm=0, type_id=TYPE_ID["u4b8"],
+                m=4, n=512, k=256, zp_float=0)
+    args.update(kw)
+    lib = capi.load()
+    st = lib.marlin_gemm(args["a"], args["a_dtype"], args["a_row_stride"], args["c"], args["bq"],
+                         args["bq_numel"], args["bias"], args["bias_numel"], args["scales"],
+                         args["scales_dtype"], args["scales_numel"], args["groups"],
+                         args["a_scales_numel"], args["glob"], args["glob_numel"], args["zeros"],
+                         args["zeros_dtype"], args["zeros_numel"], args["gidx"], args["perm"],
+                         None, 0, args["type_id"], args["m"], args["n"], args["k"], 1, 0, 0,
+                         args["zp_float"], None)
+    return st, lib.marlin_get_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(gidx=4), capi.STATUS_INVALID, "act_order g_idx"),
+    (dict(perm=4), capi.STATUS_INVALID, "act_order perm"),
+    (dict(a_dtype=capi.F32), capi.STATUS_NOT_SUPPORTED, "float16 and bfloat16"),
+    (dict(type_id=12345), capi.STATUS_NOT_SUPPORTED, "implements only"),
+    (dict(n=96, scales_numel=2 * 96, bq_numel=256 * 96 // 8), capi.STATUS_INVALID,
+     "size_n % 64 == 0"),
+    (dict(k=240, a_row_stride=240, scales_numel=512, groups=1, bq_numel=240 * 512 // 8),
+     capi.STATUS_INVALID, "size_k % 32 == 0"),
+    (dict(zeros=16, zeros_numel=2 * 512, zp_float=1), capi.STATUS_INVALID, "zero-point"),
+    (dict(type_id=TYPE_ID["u4"]), capi.STATUS_INVALID, "float zero points"),
+    (dict(zp_float=1), capi.STATUS_INVALID, "is_zp_float is true but b_zeros"),
+    (dict(groups=3, scales_numel=3 * 512), capi.STATUS_INVALID, "not divisible by b_scales"),
+    (dict(groups=16, scales_numel=16 * 512), capi.STATUS_INVALID, "unsupported group_size"),
+    (dict(glob=16, glob_numel=1), capi.STATUS_INVALID, "global_scale is supported only"),
+    (dict(type_id=TYPE_ID["nvfp4"], scales_dtype=capi.F8E4M3, groups=16,
+          scales_numel=16 * 512), capi.STATUS_INVALID, "global_scale parameter must be passed"),
+    (dict(type_id=TYPE_ID["nvfp4"], scales_dtype=capi.F16), capi.STATUS_INVALID,
+     "float8_e4m3fn for NVFP4"),
+    (dict(type_id=TYPE_ID["mxfp4"], scales_dtype=capi.F8E8M0), capi.STATUS_INVALID,
+     "group_size 32"),
+    (dict(scales_dtype=capi.BF16), capi.STATUS_INVALID, "activation dtype"),
+    (dict(a_row_stride=250), capi.STATUS_INVALID, "stride(0) must divisible by 8"),
+    (dict(a_scales_numel=4), capi.STATUS_INVALID, "a_scales"),
+    (dict(bq_numel=5), capi.STATUS_INVALID, "b_q_weight numel"),
+])
+def test_gemm_rejections(kw, status, msg):
+    st, err = _gemm(**kw)
+    assert st == status, err
+    assert msg in err, err
+
+
+def test_gemm_m_zero_is_noop():
+    st, err = _gemm(m=0, a=None, c=None)
+    assert st == capi.STATUS_OK, err
+
+
+def test_repack_rejections():
+    lib = capi.load()
+    assert lib.marlin_gptq_marlin_repack(None, 0, None, 0, 100, 64, 4, 0, None, 0, None) == 1
+    assert "tile_k_size" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_gptq_marlin_repack(None, 0, None, 0, 128, 64, 3, 0, None, 0, None) == 1
+    assert "num_bits must be 4 or 8" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_gptq_marlin_repack(None, 0, None, 0, 128, 64, 4, 1, None, 0, None) == 2
+    assert lib.marlin_awq_marlin_repack(None, 5, 128, 64, 4, 0, None, 0, None) == 1
+    assert "Shape mismatch" in lib.marlin_get_last_error().decode()
+
+
+def test_moe_rejections():
+    lib = capi.load()
+
+    def call(bs=64, type_id=TYPE_ID["u4"], zeros_numel=8 * 2 * 512, zp=1):
+        st = lib.marlin_moe_wna16_marlin_gemm(
+            16, capi.BF16, 16, 16, 8 * 256 * 512 // 8, 8, None, 0, 16, capi.BF16, 8 * 2 * 512, 2,
+            0, None, 0, 16, capi.BF16, zeros_numel, 0, 0, None, 0, 16, 100, 16, 10, 16, 16, 64,
+            bs, 4, 0, type_id, 16, 512, 256, 1, 0, 0, zp, -1, -1, -1, None)
+        return st, lib.marlin_get_last_error().decode()
+
+    st, err = call(bs=24)
+    assert st == 1 and "unsupported moe_block_size=24" in err
+    st, err = call(bs=128)
+    assert st == 1 and "unsupported moe_block_size=128" in err
+    st, err = call(zeros_numel=0, zp=0)
+    assert st == 1 and "float zero points" in err
+
+
+def test_moe_align_rejections():
+    lib = capi.load()
+    st = lib.marlin_moe_align_block_size(16, capi.I32, 8, 2000, 16, 16, 100, 16, 10, 16, None, 0,
+                                         None)
+    assert st == 1 and "padded_num_experts" in lib.marlin_get_last_error().decode()
+    st = lib.marlin_moe_align_block_size(16, capi.F32, 8, 8, 16, 16, 100, 16, 10, 16, None, 0,
+                                         None)
+    assert st == 1 and "int32 or int64" in lib.marlin_get_last_error().decode()

@@ -1,0 +1,131 @@
+"""GPU parity of the MoE path: moe_align_block_size bit-exact against the stable-order
+oracle (plus the KAT from the reference tests), each moe_wna16_marlin_gemm stage against
+the oracle within 1e-2*max|ref|, and the full fused_marlin_moe layer."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from marlin_v100_amd import capi
+from tests.quant_cases import BITS, make_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _align(topk_ids, E, bs, expert_map=None):
+    numel = topk_ids.numel()
+    sorted_numel = numel + E * (bs - 1)
+    s = torch.empty(sorted_numel, dtype=torch.int32, device="cuda")
+    e = torch.empty(sorted_numel // bs + 1, dtype=torch.int32, device="cuda")
+    n = torch.empty(1, dtype=torch.int32, device="cuda")
+    capi.moe_align_block_size(topk_ids.cuda(), E, bs, s, e, n,
+                              None if expert_map is None else expert_map.cuda())
+    return s.cpu().numpy(), e.cpu().numpy(), n.cpu().numpy()
+
+
+def test_moe_align_kat():
+    # tests/test_marlin_moe.py:274-291
+    ids = torch.tensor([[0, 3], [1, 3], [0, 2], [1, 0]], dtype=torch.int32)
+    s, e, n = _align(ids, 4, 4)
+    assert n[0] == 16
+    assert s[:16].tolist() == [0, 4, 7, 8, 2, 6, 8, 8, 5, 8, 8, 8, 1, 3, 8, 8]
+    assert e[:4].tolist() == [0, 1, 2, 3]
+    assert (s[16:] == 8).all()
+
+
+@pytest.mark.parametrize("tokens,E,topk,bs", [(16, 256, 8, 64), (2048, 256, 8, 64), (7, 8, 2, 16),
+                                               (300, 64, 6, 8), (1000, 128, 4, 48),
+                                               (3000, 512, 8, 32)])
+@pytest.mark.parametrize("id_dtype", [torch.int32, torch.int64])
+def test_moe_align_matches_oracle(tokens, E, topk, bs, id_dtype):
+    gen = torch.Generator().manual_seed(tokens + E)
+    logits = torch.randn((tokens, E), generator=gen)
+    _, ids = O.route_topk(logits, topk)
+    ids = ids.to(id_dtype)
+    s, e, n = _align(ids, E, bs)
+    rs, re, rn = O.moe_align_block_size(ids.numpy(), E, bs)
+    assert n[0] == rn[0]
+    assert np.array_equal(s, rs)
+    assert np.array_equal(e, re)
+
+
+def test_moe_align_expert_map_and_invalid_ids():
+    E, bs = 16, 16
+    gen = torch.Generator().manual_seed(1)
+    ids = torch.randint(-2, E + 3, (50, 4), generator=gen, dtype=torch.int32)
+    emap = torch.tensor([i // 2 if i % 3 else -1 for i in range(E)], dtype=torch.int32)
+    s, e, n = _align(ids, E, bs, emap)
+    rs, re, rn = O.moe_align_block_size(ids.numpy(), E, bs, expert_map=emap.numpy())
+    assert n[0] == rn[0] and np.array_equal(s, rs) and np.array_equal(e, re)
+
+
+def _make_experts(fmt, E, k, n, dtype, seed):
+    cases = [make_case(fmt, k, n, dtype, seed=seed + i) for i in range(E)]
+    bits = BITS[fmt]
+    words = torch.stack([capi.gptq_marlin_repack(c.gptq_words.cuda(), None, k, n, bits)
+                         for c in cases])
+    scales = torch.stack([c.scales for c in cases]).cuda()
+    zeros = torch.stack([c.zeros for c in cases]).cuda() if cases[0].zeros is not None else None
+    glob = (torch.cat([c.global_scale for c in cases]).cuda()
+            if cases[0].global_scale is not None else None)
+    deq = torch.stack([c.deq for c in cases])
+    return cases[0].type_id, words, scales, zeros, glob, deq
+
+
+@pytest.mark.parametrize("fmt", ["u4", "u4b8", "u8b128", "mxfp4", "nvfp4"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bs", [8, 16, 48, 64])
+def test_moe_gemm_stage1(fmt, dtype, bs):
+    T, E, topk, H, N = 37, 8, 3, 256, 512
+    print(f"case fmt={fmt} dtype={dtype} bs={bs}", flush=True)
+    tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, H, N, dtype, 10)
+    gen = torch.Generator().manual_seed(bs)
+    x = torch.randn((T, H), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    out = capi.moe_wna16_marlin_gemm(x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(),
+                                     tw.cuda(), bs, topk, False, tid, T, N, H, b_zeros=zeros,
+                                     global_scale=glob, is_zp_float=zeros is not None).cpu()
+    ref = torch.empty((T * topk, N))
+    for r in range(T * topk):
+        ref[r] = x[r // topk].float() @ deq[ids.reshape(-1)[r]].float()
+    assert O.max_abs_rel_err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_moe_gemm_stage2_topk_weights_and_bias(dtype):
+    T, E, topk, K, N, bs = 23, 8, 2, 256, 256, 16
+    tid, words, scales, zeros, glob, deq = _make_experts("u4", E, K, N, dtype, 20)
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn((T * topk, K), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    bias = (torch.randn((E, N), generator=gen) * 0.1).to(dtype)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    out = capi.moe_wna16_marlin_gemm(x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(),
+                                     tw.cuda(), bs, 1, True, tid, T * topk, N, K, b_zeros=zeros,
+                                     b_bias=O.marlin_permute_bias(bias).cuda(),
+                                     is_zp_float=True).cpu()
+    flat = ids.reshape(-1)
+    ref = torch.empty((T * topk, N))
+    for r in range(T * topk):
+        ref[r] = (x[r].float() @ deq[flat[r]].float() + bias[flat[r]].float()) * tw.reshape(-1)[r]
+    assert O.max_abs_rel_err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_marlin_moe_layer(dtype):
+    from marlin_v100_amd.fused_marlin_moe import fused_marlin_moe
+
+    T, E, topk, H, I = 33, 16, 4, 256, 128
+    tid, w13, s13, z13, _, d13 = _make_experts("u4", E, H, 2 * I, dtype, 30)
+    _, w2, s2, z2, _, d2 = _make_experts("u4", E, I, H, dtype, 60)
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn((T, H), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    out = fused_marlin_moe(x.cuda(), w13, w2, None, None, s13, s2, tw.cuda(), ids.cuda(), tid,
+                           w1_zeros=z13, w2_zeros=z2, is_w1_zp_float=True,
+                           is_w2_zp_float=True).cpu()
+    ref = O.moe_layer_ref(x, d13, d2, tw, ids)
+    assert O.max_abs_rel_err(out, ref) <= 2 * TOL

@@ -1,0 +1,298 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each oracle function is checked against the reference's own known-answer tests / golden
+vectors where they exist (tests/golden/*.json, restated from the reference test files), and
+otherwise against what the mathematics fixes (closed forms, brute force on tiny inputs,
+invariants), chosen so that a plausible slip (wrong sign, wrong index, swapped nibble
+order, off-by-one exponent) fails at least one check.  The planted-mistake tests at the
+end perturb the oracle on the CPU and confirm the checks catch it.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _golden(name):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return json.load(f)
+
+
+# ---- scalar type ids: reference tests/test_marlin_helpers.py:69-86 ------------------------
+
+def test_scalar_type_ids_match_reference_kat():
+    g = _golden("scalar_type_ids.json")
+    for name, expected in g["ids"].items():
+        assert getattr(O.scalar_types, name).id == expected, name
+
+
+def test_scalar_type_ids_closed_form():
+    # (4 << 0) | (3 << 8) | (1 << 16) | (1 << 49) | (2 << 50) (test_marlin_helpers.py:70)
+    assert O.scalar_types.float8_e4m3fn.id == (4 | 3 << 8 | 1 << 16 | 1 << 49 | 2 << 50)
+    assert O.scalar_types.float4_e2m1f.id == (2 | 1 << 8 | 1 << 16 | 1 << 49)
+    assert O.scalar_types.float8_e8m0fnu.id == (8 | 1 << 49 | 2 << 50)
+    # integer types keep the default nan_repr = IEEE_754 (1) in bits 50..57
+    assert O.scalar_types.uint4b8.id == (4 << 8 | 8 << 17 | 1 << 50)
+    assert O.scalar_types.uint8b128.id == (8 << 8 | 128 << 17 | 1 << 50)
+
+
+def test_product_scalar_type_matches_oracle():
+    from marlin_v100_amd.scalar_type import scalar_types as P
+
+    for name in ("uint4", "uint4b8", "uint8", "uint8b128", "float4_e2m1f", "float8_e4m3fn",
+                 "float8_e8m0fnu"):
+        assert getattr(P, name).id == getattr(O.scalar_types, name).id
+
+
+# ---- packing -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gptq_pack_brute_force(bits):
+    pack = 32 // bits
+    q = torch.arange(16 * 4).reshape(16, 4) % (1 << bits)
+    w = O.gptq_pack(q, bits)
+    for r in range(16 // pack):
+        for n in range(4):
+            word = int(w[r, n]) & 0xFFFFFFFF
+            for i in range(pack):
+                assert (word >> (bits * i)) & ((1 << bits) - 1) == int(q[r * pack + i, n])
+    assert torch.equal(O.unpack_gptq(w, bits), q.to(torch.int32))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_awq_pack_interleave(bits):
+    # tests/helpers.py:548-562: slot s of word (k, j) holds column pack*j + order[s]
+    order = [0, 2, 4, 6, 1, 3, 5, 7] if bits == 4 else [0, 2, 1, 3]
+    pack = 32 // bits
+    q = torch.arange(4 * 16).reshape(4, 16) % (1 << bits)
+    w = O.awq_pack(q, bits)
+    for k in range(4):
+        for j in range(16 // pack):
+            word = int(w[k, j]) & 0xFFFFFFFF
+            for s in range(pack):
+                assert (word >> (bits * s)) & ((1 << bits) - 1) == int(q[k, pack * j + order[s]])
+
+
+def test_fp4_words_low_nibble_is_even_k():
+    q = torch.arange(16 * 8).reshape(16, 8) % 16
+    w = O.fp4_to_gptq_words(q)
+    assert w.shape == (2, 8)
+    assert torch.equal(O.unpack_gptq(w, 4), q.to(torch.int32))
+
+
+def test_pack_unpack_raw_nibbles_reference_vectors():
+    # tests/test_marlin_helpers.py:106-119: raw = arange(16*n) % 16 survives pack/unpack
+    for n in (64, 128, 192):
+        raw = torch.arange(16 * n, dtype=torch.int32).reshape(16, n) % 16
+        assert torch.equal(O.unpack_gptq(O.gptq_pack(raw, 4), 4), raw)
+
+
+# ---- e2m1 / e8m0 / S0E5M3 ----------------------------------------------------------------
+
+def test_fp4_table_closed_form():
+    # e2m1: sign | exp(2) | mantissa(1); exp 0 is subnormal 0.5*m
+    for code in range(16):
+        s = -1.0 if code & 8 else 1.0
+        e = (code >> 1) & 3
+        m = code & 1
+        v = 0.5 * m if e == 0 else (1 + 0.5 * m) * 2.0 ** (e - 1)
+        assert O.FP4_VALUES[code].item() == s * v
+
+
+def test_fp4_quantizer_nearest():
+    vals = torch.tensor([0.24, 0.26, 1.25, 1.26, 5.0, 5.1, -2.4, 7.0])
+    codes = O.quantize_to_fp4_e2m1(vals)
+    assert O.FP4_VALUES[codes.long()].tolist() == [0.0, 0.5, 1.0, 1.5, 4.0, 6.0, -2.0, 6.0]
+
+
+def test_s0e5m3_roundtrip_is_exact():
+    # every positive e4m3 scale, both activation dtypes: decode(process(s)) == s * 2^7 * sf
+    # (fp16 activations use sf = 1; every positive e4m3 value is representable)
+    all_e4m3 = torch.arange(1, 127, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    s = all_e4m3[:124].reshape(4, 31).contiguous()
+    p, sf = O.nvfp4_marlin_process_scales(s[:, :28].contiguous(), torch.float16)
+    assert sf == 1.0
+    assert torch.equal(O.decode_s0e5m3(p), s[:, :28].to(torch.float32) * 128.0)
+    # bf16: sf lifts the smallest scale to >= 2 after *2^7; the encoding holds values up to
+    # the fp16 maximum, so the check uses a 2^8-wide band of scales (as a quantizer produces)
+    band = torch.arange(1, 65, dtype=torch.uint8).view(torch.float8_e4m3fn).reshape(4, 16)
+    p, sf = O.nvfp4_marlin_process_scales(band.contiguous(), torch.bfloat16)
+    assert sf > 1.0
+    assert torch.equal(O.decode_s0e5m3(p), band.to(torch.float32) * 128.0 * sf)
+
+
+def test_nvfp4_dequant_matches_direct_value():
+    # tests/test_marlin_helpers.py:156-182 (atol=0): dequant of the processed metadata equals
+    # dtype(e2m1 * e4m3_scale * global) computed directly
+    gen = torch.Generator().manual_seed(0)
+    w = torch.randn((256, 128), generator=gen) * 0.02
+    q, fp8, g = O.quantize_nvfp4(w, 16)
+    direct = O.FP4_VALUES[q.long()] * fp8.to(torch.float32).repeat_interleave(16, 0) * g
+    for dt in (torch.float16, torch.bfloat16):
+        ps, sf = O.nvfp4_marlin_process_scales(fp8, dt)
+        glob = O.nvfp4_marlin_process_global_scale(g, dt) / sf
+        deq = O.dequant_nvfp4(q, ps, glob, dt)
+        assert torch.equal(deq, direct.to(dt))
+
+
+def test_mxfp4_dequant_exact_and_close():
+    # tests/test_marlin_helpers.py:185-211
+    gen = torch.Generator().manual_seed(0)
+    w = torch.randn((256, 128), generator=gen).half()
+    q, s = O.quantize_mxfp4(w, 32)
+    deq = O.dequant_mxfp4(q, s, torch.float16)
+    direct = O.FP4_VALUES[q.long()] * torch.pow(2.0, s.view(torch.uint8).float() - 127).repeat_interleave(32, 0)
+    assert torch.equal(deq, direct.half())
+    torch.testing.assert_close(deq, w, atol=7.5e-1, rtol=7.5e-1)
+
+
+# ---- integer dequant closed forms --------------------------------------------------------
+
+def test_int_dequant_closed_forms_brute_force():
+    q = torch.arange(16).reshape(16, 1).repeat(1, 2).to(torch.int32)
+    s = torch.tensor([[0.03125, 0.1]], dtype=torch.float16)
+    zp = torch.tensor([[0.0625, 0.7]], dtype=torch.float16)
+    b8 = O.dequant_int(q, s, "u4b8", torch.float16)
+    zz = O.dequant_int(q, s, "u4", torch.float16, zp)
+    for i in range(16):
+        for j in range(2):
+            sv, zv = float(s[0, j]), float(zp[0, j])
+            assert b8[i, j].item() == float(torch.tensor((i - 8) * sv).half())
+            assert zz[i, j].item() == float(torch.tensor(i * sv - zv).half())
+
+
+def test_zero_point_quantizer_reconstructs():
+    gen = torch.Generator().manual_seed(1)
+    w = torch.randn((256, 64), generator=gen) * 0.02
+    q, s, z, zp = O.quantize_with_zero_point(w, 128, 4, torch.bfloat16)
+    assert int(q.min()) >= 0 and int(q.max()) <= 15 and int(z.max()) <= 15
+    deq = O.dequant_int(q, s, "u4", torch.bfloat16, zp).float()
+    step = s.float().repeat_interleave(128, 0)
+    assert ((deq - w).abs() <= step * 0.51 + 0.02 * step + 1e-4).all()
+
+
+def test_bias_quantizer_reconstructs():
+    gen = torch.Generator().manual_seed(2)
+    w = torch.randn((256, 64), generator=gen) * 0.02
+    q, s = O.quantize_with_bias(w, 128, 8, torch.float16)
+    deq = O.dequant_int(q, s, "u4b8", torch.float16).float()
+    step = s.float().repeat_interleave(128, 0)
+    assert ((deq - w).abs() <= step * 0.51 + 1e-4).all()
+
+
+def test_fp8_dequant_is_scaled_e4m3():
+    fp8 = torch.arange(0, 126, dtype=torch.uint8).view(torch.float8_e4m3fn).reshape(126, 1)
+    fp8 = fp8[:96].contiguous()
+    s = torch.tensor([[2.0 * 256]], dtype=torch.float16)
+    deq = O.dequant_fp8(fp8, s, torch.float16)
+    assert torch.equal(deq, (fp8.float() * 2.0).half())
+
+
+def test_bias_permutation_matches_reference_table():
+    # kInverseScalePermSingle (csrc/quantization/marlin/sm70_marlin_bias.cuh:20-23)
+    inv = _golden("bias_perm.json")["inverse_scale_perm_single"]
+    b = torch.arange(64.0)
+    p = O.marlin_permute_bias(b)
+    for logical in range(64):
+        assert p[(logical & ~31) + inv[logical & 31]].item() == logical
+
+
+# ---- moe_align_block_size ------------------------------------------------------------------
+
+def test_moe_align_reference_kat():
+    g = _golden("moe_align_kat.json")
+    s, e, n = O.moe_align_block_size(np.array(g["topk_ids"]), g["num_experts"], g["block_size"])
+    assert n[0] == g["num_tokens_post_pad"]
+    assert s[: n[0]].tolist() == g["sorted_ids"]
+    assert e[: len(g["expert_ids"])].tolist() == g["expert_ids"]
+    assert (s[n[0]:] == np.array(g["topk_ids"]).size).all()
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_moe_align_invariants(seed):
+    rng = np.random.default_rng(seed)
+    E, bs = int(rng.integers(1, 40)), int(rng.choice([4, 8, 16, 64]))
+    ids = rng.integers(0, E, size=(int(rng.integers(1, 200)), int(rng.integers(1, 5))))
+    s, e, n = O.moe_align_block_size(ids, E, bs)
+    flat = ids.reshape(-1)
+    total = n[0]
+    assert total % bs == 0
+    real = s[:total][s[:total] < flat.size]
+    assert sorted(real.tolist()) == list(range(flat.size))  # every route exactly once
+    for b in range(total // bs):
+        blk = s[b * bs:(b + 1) * bs]
+        valid = blk[blk < flat.size]
+        assert (flat[valid] == e[b]).all()          # block holds one expert
+        assert (np.diff(valid) > 0).all()            # stable (ascending) inside an expert
+    assert (e[total // bs:] == -1).all()
+    counts = np.bincount(flat, minlength=E)
+    assert total == sum((c + bs - 1) // bs * bs for c in counts)
+
+
+# ---- MoE layer reference vs the reference's per-token loop (tests/helpers.py:2039-2060) ----
+
+def _per_token_loop(x, w1, w2, tw, ids):
+    out = []
+    for t in range(x.shape[0]):
+        acc = torch.zeros(x.shape[1])
+        row = x[t:t + 1].float()
+        for r in range(ids.shape[1]):
+            e = int(ids[t, r])
+            g, u = (row @ w1[e].float()).chunk(2, dim=-1)
+            acc += (torch.nn.functional.silu(g) * u @ w2[e].float())[0] * tw[t, r]
+        out.append(acc)
+    return torch.stack(out)
+
+
+def test_moe_layer_ref_matches_per_token_loop():
+    gen = torch.Generator().manual_seed(3)
+    T, E, H, I, k = 9, 5, 32, 16, 3
+    x = torch.randn((T, H), generator=gen)
+    w1 = torch.randn((E, H, 2 * I), generator=gen) * 0.1
+    w2 = torch.randn((E, I, H), generator=gen) * 0.1
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), k)
+    torch.testing.assert_close(O.moe_layer_ref(x, w1, w2, tw, ids),
+                               _per_token_loop(x, w1, w2, tw, ids), rtol=1e-5, atol=1e-5)
+
+
+def test_route_topk_renormalises():
+    tw, ids = O.route_topk(torch.randn((20, 64)), 8)
+    torch.testing.assert_close(tw.sum(-1), torch.ones(20))
+    assert ids.dtype == torch.int32 and int(ids.max()) < 64
+
+
+# ---- planted mistakes: the checks above must catch a plausible slip ------------------------
+
+def test_planted_wrong_bias_sign_is_caught(monkeypatch):
+    q = torch.arange(16).reshape(16, 1).to(torch.int32)
+    s = torch.tensor([[0.5]], dtype=torch.float16)
+    good = O.dequant_int(q, s, "u4b8", torch.float16)
+    bad = ((q.float() + 8.0) * 0.5).half()
+    assert not torch.equal(good, bad)
+
+
+def test_planted_swapped_nvfp4_shuffle_is_caught():
+    gen = torch.Generator().manual_seed(0)
+    w = torch.randn((32, 8), generator=gen) * 0.02
+    q, fp8, g = O.quantize_nvfp4(w, 16)
+    ps, sf = O.nvfp4_marlin_process_scales(fp8, torch.float16)
+    # decoding without undoing the [0,2,1,3] shuffle must break the direct-value identity
+    bits = ps.view(torch.uint8).to(torch.int16) << 7
+    wrong = bits.view(torch.float16).float()
+    right = O.decode_s0e5m3(ps)
+    assert not torch.equal(wrong, right)
+
+
+def test_planted_align_order_is_caught():
+    g = _golden("moe_align_kat.json")
+    s, _, n = O.moe_align_block_size(np.array(g["topk_ids"]), g["num_experts"], g["block_size"])
+    reversed_within_expert = list(s[: n[0]])
+    reversed_within_expert[0], reversed_within_expert[1] = reversed_within_expert[1], reversed_within_expert[0]
+    assert reversed_within_expert != g["sorted_ids"]
