@@ -1,0 +1,351 @@
+"""Benchmark of the Marlin hot path on one MI355X.
+
+Headline (`value`): weight GB/s of marlin_gemm on BASELINE configs[1] -- AWQ-style uint4 +
+float zero point, group 128, bf16 activations, K=5120, N=34816 -- at M=16 (decode).  One
+"step" is one marlin_gemm call on that workload with all inputs resident in HBM.  Weight
+copies rotate through >= 512 MiB so the 256 MB Infinity Cache cannot hold them.
+
+The same JSON line carries every other BASELINE configuration (`configs`): cfg1 u4b8 fp16,
+cfg2 at M in {1,16,128,1024}, cfg3 u8b128 M=4096 (MFMA bound), cfg4 MXFP4/NVFP4 at
+M in {1,64,512}, and the cfg5 MoE layer (align + 2 grouped GEMMs + activation + top-k sum)
+at T in {16, 2048}; plus `roofline` for the headline kernel and `cpu_baseline` (the
+reference's CPU path: dequantize then fp32 matmul, timed on the host cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16/fp16
+ROTATE_BYTES = 512 << 20
+
+METRIC = "marlin_gemm weight GB/s + TFLOPS vs roofline, M=1..4096; MoE layer µs"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of config keys to run")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------------------
+# synthetic quantized weights, built on the GPU (input generation, not the measured path)
+# ---------------------------------------------------------------------------------------
+
+def _pack_gptq(q, bits):
+    import torch
+
+    k, n = q.shape
+    pack = 32 // bits
+    qn = q.to(torch.int64).reshape(k // pack, pack, n)
+    out = torch.zeros((k // pack, n), dtype=torch.int64, device=q.device)
+    for i in range(pack):
+        out |= qn[:, i, :] << (bits * i)
+    out = torch.where(out >= 2 ** 31, out - 2 ** 32, out)
+    return out.to(torch.int32)
+
+
+FP4_GRID = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+
+
+def make_weights(fmt, k, n, dtype, gen, experts=None):
+    """RTN-quantize W ~ N(0, 0.02) [K, N] in `fmt`; returns dict of kernel operands."""
+    import torch
+
+    from marlin_v100_amd import ops
+    from marlin_v100_amd.marlin_utils import (nvfp4_marlin_process_global_scale,
+                                              nvfp4_marlin_process_scales)
+
+    w = (torch.randn((k, n), generator=gen, device="cuda") * 0.02)
+    out = {}
+    if fmt == "u4b8":
+        g = k // 128
+        r = w.reshape(g, 128, n)
+        s = (r.abs().amax(1) / 7).clamp_min(1e-6).to(dtype)
+        q = (torch.round(r / s.float().unsqueeze(1)).clamp(-8, 7) + 8).reshape(k, n)
+        out.update(words=_pack_gptq(q, 4), scales=s, bits=4)
+    elif fmt == "u4":
+        g = k // 128
+        r = w.reshape(g, 128, n)
+        mn, mx = r.amin(1), r.amax(1)
+        s32 = ((mx - mn) / 15).clamp_min(1e-6)
+        z = torch.round(-mn / s32).clamp(0, 15)
+        q = torch.round(r / s32.unsqueeze(1) + z.unsqueeze(1)).clamp(0, 15).reshape(k, n)
+        s = s32.to(dtype)
+        out.update(words=_pack_gptq(q, 4), scales=s, zeros=(z * s.float()).to(dtype), bits=4)
+    elif fmt == "u8b128":
+        s = (w.abs().amax(0, keepdim=True) / 127).clamp_min(1e-6).to(dtype)
+        q = torch.round(w / s.float()).clamp(-128, 127) + 128
+        out.update(words=_pack_gptq(q, 8), scales=s, bits=8)
+    elif fmt in ("mxfp4", "nvfp4"):
+        gs = 32 if fmt == "mxfp4" else 16
+        r = w.reshape(k // gs, gs, n)
+        grid = torch.tensor(FP4_GRID, device="cuda")
+        amax = r.abs().amax(1)
+        if fmt == "mxfp4":
+            e = torch.ceil(torch.log2((amax / 6).clamp_min(2.0 ** -127)))
+            sc = torch.pow(2.0, e).to(torch.float8_e8m0fnu)
+            eff = sc.float()
+        else:
+            sc32 = (amax / 6).clamp_min(1e-6)
+            glob = (sc32.max() / 448).reshape(1)
+            sc = (sc32 / glob).to(torch.float8_e4m3fn)
+            eff = sc.float() * glob
+        x = r / eff.unsqueeze(1)
+        q = (x.unsqueeze(-1) - grid).abs().argmin(-1).reshape(k, n)
+        words = _pack_gptq(q, 4)
+        if fmt == "mxfp4":
+            out.update(words=words, scales=sc.contiguous(), bits=4)
+        else:
+            ps, sf = nvfp4_marlin_process_scales(sc, a_dtype=dtype)
+            gsc = (nvfp4_marlin_process_global_scale(glob, dtype) / sf).float()
+            out.update(words=words, scales=ps, global_scale=gsc, bits=4)
+    else:
+        raise ValueError(fmt)
+    out["qweight"] = ops.gptq_marlin_repack(out.pop("words"), torch.empty(0, dtype=torch.int32,
+                                                                           device="cuda"),
+                                            k, n, out["bits"])
+    return out
+
+
+def meta_bytes(wt):
+    b = wt["qweight"].numel() * 4
+    for key in ("scales", "zeros", "global_scale"):
+        if wt.get(key) is not None:
+            b += wt[key].numel() * wt[key].element_size()
+    return b
+
+
+# ---------------------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------------------
+
+def time_calls(fn_list, steps, warmup):
+    """Average per-call device time of rotating calls, HIP events on the current stream."""
+    import torch
+
+    n = len(fn_list)
+    for i in range(warmup):
+        fn_list[i % n]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn_list[i % n]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
+    import torch
+
+    from marlin_v100_amd import ops
+    from marlin_v100_amd.scalar_type import scalar_types
+
+    qtype = {"u4b8": scalar_types.uint4b8, "u4": scalar_types.uint4,
+             "u8b128": scalar_types.uint8b128, "mxfp4": scalar_types.float4_e2m1f,
+             "nvfp4": scalar_types.float4_e2m1f}[fmt]
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    first = make_weights(fmt, k, n, dtype, gen)
+    wbytes = meta_bytes(first)
+    copies = max(1, min(8, -(-ROTATE_BYTES // wbytes)))
+    weights = [first] + [make_weights(fmt, k, n, dtype, gen) for _ in range(copies - 1)]
+    a = torch.randn((m, k), generator=gen, device="cuda").to(dtype)
+    c = torch.empty((m, n), device="cuda", dtype=dtype)
+    ws = torch.empty(0, dtype=torch.int32, device="cuda")
+
+    def call(wt):
+        return lambda: ops.marlin_gemm(a, c, wt["qweight"], None, wt["scales"], None,
+                                       wt.get("global_scale"), wt.get("zeros"), None, None, ws,
+                                       qtype, m, n, k, True, False, False,
+                                       wt.get("zeros") is not None)
+
+    fns = [call(wt) for wt in weights]
+    t = time_calls(fns, steps, warmup)
+    alg_bytes = wbytes + a.numel() * 2 + c.numel() * 2
+    flops = 2.0 * m * n * k
+    gbs = alg_bytes / t / 1e9
+    tflops = flops / t / 1e12
+    bound = "hbm" if alg_bytes / (HBM_PEAK_GBS * 1e9) >= flops / (MFMA_PEAK_TFLOPS * 1e12) else "mfma"
+    return {
+        "key": key, "fmt": fmt, "dtype": str(dtype).replace("torch.", ""), "M": m, "K": k, "N": n,
+        "us": round(t * 1e6, 2), "weight_GBs": round(wbytes / t / 1e9, 1),
+        "alg_GBs": round(gbs, 1), "TFLOPs": round(tflops, 2), "bound": bound,
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+        "alg_bytes": alg_bytes, "weight_bytes": wbytes, "flops": flops, "rotated_copies": copies,
+    }
+
+
+def moe_case(key, tokens, steps, warmup, seed):
+    """cfg5: E=256, top-8, H=3072, I=1536, uint4 + float zp g128, bf16, block 64."""
+    import torch
+
+    from marlin_v100_amd.fused_marlin_moe import fused_marlin_moe
+    from marlin_v100_amd.scalar_type import scalar_types
+
+    E, topk, H, I, bs = 256, 8, 3072, 1536, 64
+    dtype = torch.bfloat16
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    w13 = [make_weights("u4", H, 2 * I, dtype, gen) for _ in range(E)]
+    w2 = [make_weights("u4", I, H, dtype, gen) for _ in range(E)]
+    q13 = torch.stack([w["qweight"] for w in w13]); s13 = torch.stack([w["scales"] for w in w13])
+    z13 = torch.stack([w["zeros"] for w in w13])
+    q2 = torch.stack([w["qweight"] for w in w2]); s2 = torch.stack([w["scales"] for w in w2])
+    z2 = torch.stack([w["zeros"] for w in w2])
+    del w13, w2
+    x = torch.randn((tokens, H), generator=gen, device="cuda").to(dtype)
+    logits = torch.randn((tokens, E), generator=gen, device="cuda")
+    p = torch.softmax(logits, -1)
+    tw, ids = torch.topk(p, topk, -1)
+    tw = (tw / tw.sum(-1, keepdim=True)).float().contiguous()
+    ids = ids.to(torch.int32).contiguous()
+    qid = scalar_types.uint4.id
+
+    def fn():
+        return fused_marlin_moe(x, q13, q2, None, None, s13, s2, tw, ids, qid, w1_zeros=z13,
+                                w2_zeros=z2, is_w1_zp_float=True, is_w2_zp_float=True,
+                                block_size_m=bs)
+
+    t = time_calls([fn], steps, warmup)
+    touched = int(torch.unique(ids).numel())
+    per_expert = (q13[0].numel() + q2[0].numel()) * 4 + (s13[0].numel() + z13[0].numel()
+                                                         + s2[0].numel() + z2[0].numel()) * 2
+    alg_bytes = touched * per_expert + 2 * tokens * H * 2
+    flops = 2.0 * tokens * topk * (H * 2 * I + I * H)
+    roof = max(alg_bytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_TFLOPS * 1e12))
+    return {"key": key, "T": tokens, "E": E, "topk": topk, "H": H, "I": I, "block": bs,
+            "layer_us": round(t * 1e6, 2), "touched_experts": touched, "alg_bytes": alg_bytes,
+            "flops": flops, "roofline_us": round(roof * 1e6, 2),
+            "vs_roofline": round(t / roof, 3)}
+
+
+# ---------------------------------------------------------------------------------------
+# CPU reference path (bounded sample), timed on the host cores
+# ---------------------------------------------------------------------------------------
+
+def cpu_baseline(m, k, n):
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle as O
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(1001)
+    # bounded sample: the full K, a 4096-column slice of N (weights dominate the work)
+    ns = min(n, 4096)
+    w = torch.randn((k, ns), generator=gen) * 0.02
+    q, s, _z, zp = O.quantize_with_zero_point(w, 128, 4, torch.bfloat16)
+    a = torch.randn((m, k), generator=gen).bfloat16()
+
+    def run():
+        deq = O.dequant_int(q, s, "u4", torch.bfloat16, zp)
+        return O.gemm_ref(a, deq)
+
+    run()
+    times = []
+    t_end = time.time() + 20.0
+    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    wbytes = k * ns // 2 + 2 * (k // 128) * ns * 2
+    return {"value": round(wbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"oracle dequant (uint4+zp g128 -> bf16) + fp32 torch.matmul, "
+                      f"M={m} K={k} N={ns} (column slice of N={n}), median of {len(times)} runs",
+            "ms_per_call": round(t * 1e3, 2)}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    from marlin_v100_amd import ops  # noqa: F401  (loads the native libraries; no fallback)
+
+    only = set(filter(None, args.only.split(",")))
+    bf, hf = torch.bfloat16, torch.float16
+    head = dense_case("cfg2_m16", "u4", 16, 5120, 34816, bf, args.steps, args.warmup, 1002)
+
+    plan = [
+        ("cfg1_m16", "u4b8", 16, 4096, 4096, hf, 1001),
+        ("cfg2_m1", "u4", 1, 5120, 34816, bf, 1002),
+        ("cfg2_m128", "u4", 128, 5120, 34816, bf, 1002),
+        ("cfg2_m1024", "u4", 1024, 5120, 34816, bf, 1002),
+        ("cfg3_m4096", "u8b128", 4096, 8192, 8192, hf, 1003),
+        ("cfg4_mxfp4_m1", "mxfp4", 1, 3072, 12288, bf, 1004),
+        ("cfg4_mxfp4_m64", "mxfp4", 64, 3072, 12288, bf, 1004),
+        ("cfg4_mxfp4_m512", "mxfp4", 512, 3072, 12288, bf, 1004),
+        ("cfg4_nvfp4_m1", "nvfp4", 1, 3072, 12288, bf, 1004),
+        ("cfg4_nvfp4_m64", "nvfp4", 64, 3072, 12288, bf, 1004),
+        ("cfg4_nvfp4_m512", "nvfp4", 512, 3072, 12288, bf, 1004),
+    ]
+    configs = {"cfg2_m16": head}
+    if not args.quick:
+        for key, fmt, m, k, n, dt, seed in plan:
+            if only and key not in only:
+                continue
+            steps = max(20, args.steps // (4 if m >= 1024 else 1))
+            configs[key] = dense_case(key, fmt, m, k, n, dt, steps, args.warmup, seed)
+            print(f"# {key}: {configs[key]['us']} us", file=sys.stderr, flush=True)
+        for key, t in (("cfg5_moe_t16", 16), ("cfg5_moe_t2048", 2048)):
+            if only and key not in only:
+                continue
+            configs[key] = moe_case(key, t, max(10, args.steps // 10), max(3, args.warmup // 4), 1005)
+            print(f"# {key}: {configs[key]['layer_us']} us", file=sys.stderr, flush=True)
+
+    t = head["us"] / 1e6
+    line = {
+        "metric": METRIC,
+        "value": head["weight_GBs"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (W ~ N(0,0.02) RTN-quantized on device, A ~ N(0,1))",
+        "config": {"workload": "cfg2: marlin_gemm uint4+zp g128 bf16, M=16 K=5120 N=34816 "
+                               "(AWQ-style, decode)", "M": 16, "K": 5120, "N": 34816,
+                   "group_size": 128, "b_type": "uint4", "act": "bf16",
+                   "cold_cache_rotation_copies": head["rotated_copies"]},
+        "roofline": {"bound": "hbm", "achieved": head["alg_GBs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head["alg_GBs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "mmi::marlin_gemm_kernel<FMT_U4, BF16, 16, *, GSM_BIG, false>",
+                     "algorithmic_bytes_per_launch": head["alg_bytes"]},
+        "configs": configs,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(16, 5120, 34816)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -156,12 +156,24 @@ __device__ __forceinline__ Meta make_meta(uint32_t raw) {
     m.s = e8m0_to_float(raw & 0xff);
     m.s16 = m.c1 = m.c16 = 0.f;
   } else if constexpr (FMT == FMT_NVFP4) {
-    m.s = s0e5m3_to_float_div128(raw & 0xff);
-    m.s16 = m.c1 = m.c16 = 0.f;
+    // v_cvt_scalef32_pk_*_fp4 applies only the exponent of its scale operand, so the scale
+    // s*sf = 2^E * (1 + m/8) is split: s = 2^E goes to the conversion, s16 carries the full
+    // value (bf16 path) and c1 holds (1 + m/8) as an f16 pair (f16 path).
+    const float full = s0e5m3_to_float_div128(raw & 0xff);
+    const uint32_t fb = __builtin_bit_cast(uint32_t, full);
+    m.s = __builtin_bit_cast(float, fb & 0xff800000u);
+    m.s16 = full;
+    const _Float16 mant = (_Float16)__builtin_bit_cast(float, (fb & 0x007fffffu) | 0x3f800000u);
+    const f16x2_t mm = {mant, mant};
+    m.c1 = __builtin_bit_cast(float, mm);
+    m.c16 = 0.f;
   } else if constexpr (FMT == FMT_FP8) {
-    // Dequant is fp8 * (s / 256) (tests/helpers.py:1117-1121).
+    // Dequant is fp8 * (s / 256) (tests/helpers.py:1117-1121).  bf16 path: s/256 in fp32;
+    // fp16 path: the stored fp16 scale s as a packed pair in c1.
     m.s = raw16_to_float(raw & 0xffff, AT{}) * 0.00390625f;
-    m.s16 = m.c1 = m.c16 = 0.f;
+    m.s16 = 0.f;
+    m.c1 = __builtin_bit_cast(float, (raw & 0xffffu) | (raw << 16));
+    m.c16 = 0.f;
   } else {
     const float s = raw16_to_float(raw & 0xffff, AT{});
     m.s = s;
@@ -224,8 +236,17 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
                  AT{});
     r[3] = pack2(__builtin_fmaf(h_hi(b0), m.s, m.c1), __builtin_fmaf(h_hi(b1), m.s, m.c1),
                  AT{});
+  } else if constexpr (FMT == FMT_FP8 && AT::kId == 0) {
+    // fp16: e4m3fn * 2^-8 -> fp16 exactly (hardware scaled conversion, power-of-two scale),
+    // then one packed fp16 multiply by s: a single rounding of the exact fp8 * s / 256.
+    const f16x2_t s2 = __builtin_bit_cast(f16x2_t, m.c1);
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 0.00390625f, false) * s2);
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 0.00390625f, true) * s2);
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 0.00390625f, false) * s2);
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 0.00390625f, true) * s2);
   } else if constexpr (FMT == FMT_FP8) {
-    // OCP e4m3fn -> fp32 exactly, times s/256 (exact: <= 15 significant bits), one rounding.
+    // bf16: OCP e4m3fn -> fp32 exactly, times s/256 (exact: <= 15 significant bits), one
+    // rounding in the conversion to bf16.
     const f32x2_t p0 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
     const f32x2_t p1 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
     const f32x2_t p2 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
@@ -234,10 +255,33 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
     r[1] = pack2(p1[0] * m.s, p1[1] * m.s, AT{});
     r[2] = pack2(p2[0] * m.s, p2[1] * m.s, AT{});
     r[3] = pack2(p3[0] * m.s, p3[1] * m.s, AT{});
+  } else if constexpr (FMT == FMT_NVFP4) {
+    // e2m1 (<= 2 significant bits) times the e4m3-derived scale (<= 4 significant bits) is
+    // exact in fp16/bf16.  fp16: convert with the power-of-two part, then one packed
+    // multiply by (1 + m/8).  bf16: convert to fp32 and multiply by the full scale.
+    if constexpr (AT::kId == 1) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        f32x2_t v;
+        switch (b) {
+          case 0: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w0, 1.0f, 0); break;
+          case 1: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w0, 1.0f, 1); break;
+          case 2: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w0, 1.0f, 2); break;
+          default: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w0, 1.0f, 3); break;
+        }
+        r[b] = pack2(v[0] * m.s16, v[1] * m.s16, AT{});
+      }
+    } else {
+      const f16x2_t mm = __builtin_bit_cast(f16x2_t, m.c1);
+      r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 0) * mm);
+      r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 1) * mm);
+      r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 2) * mm);
+      r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 3) * mm);
+    }
   } else {
-    // e2m1 pairs -> 16-bit with a hardware scaled conversion.  e2m1 values carry at most
-    // 2 significant bits and the scale (a power of two for MXFP4, a 4-bit-significand
-    // e4m3 value times a power of two for NVFP4) at most 4, so the product is exact.
+    // MXFP4: e2m1 pairs -> 16-bit with the hardware scaled conversion; the e8m0 scale is a
+    // power of two, which is what the conversion applies (it uses only the scale's
+    // exponent), so the result is exact.
     if constexpr (AT::kId == 1) {
       r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, m.s, 0));
       r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, m.s, 1));

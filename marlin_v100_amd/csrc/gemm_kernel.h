@@ -115,7 +115,8 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
   const int out_tile = bid;
 
   int expert = 0;
-  const AT* a = reinterpret_cast<const AT*>(p.a);
+  // activations as raw 16-bit words (AT is a tag type, not the element type)
+  const uint16_t* a = reinterpret_cast<const uint16_t*>(p.a);
   if constexpr (MOE) {
     const int padded = p.num_post_pad[0];
     if (m_blk * p.moe_bs >= padded || m_blk >= p.expert_ids_numel) return;
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
 
   // ---- activation rows this wave copies into LDS: fragments f = wave + 4*i --------------
   constexpr int FPW = FRAGS / 4;  // fragments per wave per step
-  const AT* a_src[FPW];
+  const uint16_t* a_src[FPW];
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
     const int f = wave + 4 * i;
@@ -334,8 +335,8 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
   // ---- epilogue --------------------------------------------------------------------------
   float alpha = 1.0f;
   if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[expert], p.alpha_exp);
-  const AT* bias = reinterpret_cast<const AT*>(p.bias);
-  AT* cout = reinterpret_cast<AT*>(p.c);
+  const uint16_t* bias = reinterpret_cast<const uint16_t*>(p.bias);
+  uint16_t* cout = reinterpret_cast<uint16_t*>(p.c);
 
   auto out_row = [&](int r) -> int64_t {  // -1 when the row is not stored
     if constexpr (MOE) {
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
     if constexpr (MOE) {
       if (p.mul_topk) o *= p.topk_w[orow];
     }
-    reinterpret_cast<uint16_t*>(cout)[orow * p.N + col] = to_raw16(o, AT{});
+    cout[orow * p.N + col] = to_raw16(o, AT{});
   };
 
   if (p.splits == 1) {

@@ -81,7 +81,7 @@ at::Tensor op_gptq_marlin_repack(at::Tensor& b_q_weight, at::Tensor& perm, int64
   TORCH_CHECK(perm.device().is_cuda(), "perm is not on GPU");
   TORCH_CHECK(perm.is_contiguous(), "perm is not contiguous");
   TORCH_CHECK(perm.dtype() == at::kInt, "perm type is not at::kInt");
-  const c10::hip::OptionalHIPGuard guard(b_q_weight.device());
+  const at::OptionalDeviceGuard guard(b_q_weight.device());
   at::Tensor out = torch::empty({size_k / 16, size_n * 16 / pack}, b_q_weight.options());
   rethrow(marlin_gptq_marlin_repack(b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(),
                                     perm.numel() ? perm.data_ptr<int32_t>() : nullptr,
@@ -102,7 +102,7 @@ at::Tensor op_awq_marlin_repack(at::Tensor& b_q_weight, int64_t size_k, int64_t 
   TORCH_CHECK(b_q_weight.device().is_cuda(), "b_q_weight is not on GPU");
   TORCH_CHECK(b_q_weight.is_contiguous(), "b_q_weight is not contiguous");
   TORCH_CHECK(b_q_weight.dtype() == at::kInt, "b_q_weight type is not kInt");
-  const c10::hip::OptionalHIPGuard guard(b_q_weight.device());
+  const at::OptionalDeviceGuard guard(b_q_weight.device());
   at::Tensor out = torch::empty({size_k / 16, size_n * 16 / pack}, b_q_weight.options());
   rethrow(marlin_awq_marlin_repack(b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(), size_k,
                                    size_n, num_bits, is_a_8bit, out.data_ptr<int32_t>(),
@@ -164,7 +164,7 @@ at::Tensor op_marlin_gemm(at::Tensor& a, std::optional<at::Tensor> c_or_none, at
                 b_zeros_or_none->size(0), " is not num_groups = ", b_scales.size(0));
   }
 
-  const c10::hip::OptionalHIPGuard guard(a.device());
+  const at::OptionalDeviceGuard guard(a.device());
   at::Tensor c;
   if (c_or_none.has_value()) {
     c = c_or_none.value();
@@ -209,7 +209,7 @@ at::Tensor mmi_dequantize(at::Tensor& b_q_weight, at::Tensor& b_scales,
               "b_scales must be a contiguous [num_groups, size_n] GPU tensor");
   check_cuda_contig(b_zeros_or_none, "b_zeros");
   check_cuda_contig(global_scale_or_none, "global_scale");
-  const c10::hip::OptionalHIPGuard guard(b_q_weight.device());
+  const at::OptionalDeviceGuard guard(b_q_weight.device());
   at::Tensor out = torch::empty({size_k, size_n}, b_q_weight.options().dtype(out_dtype));
   rethrow(marlin_dequantize(b_q_weight.data_ptr<int32_t>(), b_q_weight.numel(),
                             b_scales.data_ptr(), to_mdt(b_scales.scalar_type()), b_scales.numel(),
@@ -270,7 +270,7 @@ void op_moe_align_block_size(at::Tensor topk_ids, int64_t num_experts, int64_t b
                     maybe_expert_map->scalar_type() == at::kInt,
                 "expert_map must be a contiguous int32 GPU tensor");
   }
-  const c10::hip::OptionalHIPGuard guard(topk_ids.device());
+  const at::OptionalDeviceGuard guard(topk_ids.device());
   rethrow(marlin_moe_align_block_size(
       topk_ids.data_ptr(), to_mdt(topk_ids.scalar_type()), topk_ids.numel(), num_experts,
       block_size, sorted_token_ids.data_ptr<int32_t>(), sorted_token_ids.numel(),
@@ -347,7 +347,7 @@ at::Tensor op_moe_wna16_marlin_gemm(
                   topk_weights.scalar_type() == at::kFloat,
               "topk_weights must be a contiguous float32 GPU tensor");
 
-  const c10::hip::OptionalHIPGuard guard(a.device());
+  const at::OptionalDeviceGuard guard(a.device());
   at::Tensor c;
   if (c_or_none.has_value()) {
     c = c_or_none.value();
@@ -388,7 +388,7 @@ void op_moe_sum(at::Tensor& input, at::Tensor& output) {
               "output must be a contiguous [tokens, hidden] GPU tensor");
   TORCH_CHECK(output.scalar_type() == input.scalar_type(), "dtype mismatch");
   TORCH_CHECK(output.size(0) == input.size(0) && output.size(1) == input.size(2), "shape mismatch");
-  const c10::hip::OptionalHIPGuard guard(input.device());
+  const at::OptionalDeviceGuard guard(input.device());
   rethrow(marlin_moe_sum(input.data_ptr(), to_mdt(input.scalar_type()), input.size(0),
                          input.size(1), input.size(2), output.data_ptr(), cur_stream(input)));
 }

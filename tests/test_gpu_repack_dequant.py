@@ -18,23 +18,28 @@ def _dequant(case, words):
                            b_zeros=case.zeros, global_scale=case.global_scale)
 
 
-def _gs_ok(fmt, k, gs):
-    return gs == -1 or k % gs == 0
+def _gs_for(fmt, k):
+    from tests.quant_cases import DEFAULT_GS
+    gs = DEFAULT_GS[fmt]
+    if gs != -1 and k % gs:
+        gs = {"fp8": -1}.get(fmt, 32)
+    return gs
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("k,n", SHAPES)
 def test_gptq_repack_dequant_bit_exact(fmt, dtype, k, n):
-    case = make_case(fmt, k, n, dtype, seed=k + n)
-    if not _gs_ok(fmt, k, case.gs):
-        pytest.skip("group size does not divide K")
+    case = make_case(fmt, k, n, dtype, gs=_gs_for(fmt, k), seed=k + n)
     print(f"case fmt={fmt} dtype={dtype} k={k} n={n}", flush=True)
     d = to_dev(case)
     words = capi.gptq_marlin_repack(d.gptq_words, None, k, n, 8 if fmt in ("u8b128", "u8", "fp8") else 4)
     out = _dequant(d, words).cpu()
-    assert torch.equal(out.view(torch.int16), case.deq.view(torch.int16)), \
-        f"mismatch at {(out != case.deq).nonzero()[:5].tolist()}"
+    bad = (out.view(torch.int16) != case.deq.view(torch.int16)).nonzero()[:5]
+    assert bad.numel() == 0, (
+        f"mismatch at {bad.tolist()}: got bits "
+        f"{[hex(int(out.view(torch.int16)[i, j]) & 0xffff) for i, j in bad.tolist()]} want "
+        f"{[hex(int(case.deq.view(torch.int16)[i, j]) & 0xffff) for i, j in bad.tolist()]}")
 
 
 @pytest.mark.parametrize("fmt", ["u4b8", "u4", "u8b128", "u8"])
