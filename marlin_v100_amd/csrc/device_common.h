@@ -147,19 +147,25 @@ struct Meta {
   float c16;  // offset for 1024 + 16q
 };
 
-// Raw metadata for one (group, column): low 16 bits scale, high 16 bits zero point for
-// 16-bit metadata; the scale byte for fp4.
+// Raw metadata for one (group, column) as loaded: the scale bits (16-bit, or the fp4 scale
+// byte) and the float zero point bits.  The two halves stay in separate registers until
+// use, so a prefetch of the next step never has to wait for them.
+struct MetaRaw {
+  uint32_t s;
+  uint32_t z;
+};
+
 template <int FMT, class AT>
-__device__ __forceinline__ Meta make_meta(uint32_t raw) {
+__device__ __forceinline__ Meta make_meta(MetaRaw raw) {
   Meta m;
   if constexpr (FMT == FMT_MXFP4) {
-    m.s = e8m0_to_float(raw & 0xff);
+    m.s = e8m0_to_float(raw.s & 0xff);
     m.s16 = m.c1 = m.c16 = 0.f;
   } else if constexpr (FMT == FMT_NVFP4) {
     // v_cvt_scalef32_pk_*_fp4 applies only the exponent of its scale operand, so the scale
     // s*sf = 2^E * (1 + m/8) is split: s = 2^E goes to the conversion, s16 carries the full
     // value (bf16 path) and c1 holds (1 + m/8) as an f16 pair (f16 path).
-    const float full = s0e5m3_to_float_div128(raw & 0xff);
+    const float full = s0e5m3_to_float_div128(raw.s & 0xff);
     const uint32_t fb = __builtin_bit_cast(uint32_t, full);
     m.s = __builtin_bit_cast(float, fb & 0xff800000u);
     m.s16 = full;
@@ -170,12 +176,12 @@ __device__ __forceinline__ Meta make_meta(uint32_t raw) {
   } else if constexpr (FMT == FMT_FP8) {
     // Dequant is fp8 * (s / 256) (tests/helpers.py:1117-1121).  bf16 path: s/256 in fp32;
     // fp16 path: the stored fp16 scale s as a packed pair in c1.
-    m.s = raw16_to_float(raw & 0xffff, AT{}) * 0.00390625f;
+    m.s = raw16_to_float(raw.s & 0xffff, AT{}) * 0.00390625f;
     m.s16 = 0.f;
-    m.c1 = __builtin_bit_cast(float, (raw & 0xffffu) | (raw << 16));
+    m.c1 = __builtin_bit_cast(float, (raw.s & 0xffffu) | (raw.s << 16));
     m.c16 = 0.f;
   } else {
-    const float s = raw16_to_float(raw & 0xffff, AT{});
+    const float s = raw16_to_float(raw.s & 0xffff, AT{});
     m.s = s;
     m.s16 = s * 0.0625f;
     if constexpr (FMT == FMT_U4B8) {
@@ -185,7 +191,7 @@ __device__ __forceinline__ Meta make_meta(uint32_t raw) {
       m.c1 = -1152.0f * s;  // (1024 + q)*s - 1152 s = (q - 128) s
       m.c16 = 0.f;
     } else {
-      const float z = raw16_to_float(raw >> 16, AT{});
+      const float z = raw16_to_float(raw.z & 0xffff, AT{});
       m.c1 = __builtin_fmaf(-1024.0f, s, -z);  // exact: |1024 s + z| has <= 22 bits
       m.c16 = __builtin_fmaf(-64.0f, s, -z);
     }

@@ -64,20 +64,20 @@ __device__ __forceinline__ uint32_t load_u16(const void* p, int64_t idx) {
 }
 
 template <int FMT, class AT>
-__device__ __forceinline__ uint32_t load_meta_raw(const GemmParams& p, int64_t base, int group,
-                                                  int col) {
+__device__ __forceinline__ MetaRaw load_meta_raw(const GemmParams& p, int64_t base, int group,
+                                                 int col) {
   const int64_t idx = base + (int64_t)group * p.N;
   if constexpr (FMT == FMT_NVFP4) {
     // NVFP4 scales are stored with a [0,2,1,3] shuffle per 4 columns
     // (marlin_utils_fp4.py:83-86); the shuffle is its own inverse.
     const int sc = (col & ~3) | ((col & 1) << 1) | ((col & 2) >> 1);
-    return reinterpret_cast<const uint8_t*>(p.scales)[idx + sc];
+    return MetaRaw{reinterpret_cast<const uint8_t*>(p.scales)[idx + sc], 0u};
   } else if constexpr (FMT == FMT_MXFP4) {
-    return reinterpret_cast<const uint8_t*>(p.scales)[idx + col];
+    return MetaRaw{reinterpret_cast<const uint8_t*>(p.scales)[idx + col], 0u};
   } else if constexpr (fmt_has_zp(FMT)) {
-    return load_u16<AT>(p.scales, idx + col) | (load_u16<AT>(p.zeros, idx + col) << 16);
+    return MetaRaw{load_u16<AT>(p.scales, idx + col), load_u16<AT>(p.zeros, idx + col)};
   } else {
-    return load_u16<AT>(p.scales, idx + col);
+    return MetaRaw{load_u16<AT>(p.scales, idx + col), 0u};
   }
 }
 
@@ -88,8 +88,17 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, void* lds_wave_base)
 
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Waves per SIMD the register allocation must leave room for: the small-M (weight
+// streaming) tiles need many waves in flight, the 128-row tiles trade occupancy for
+// accumulators.
+template <int BM>
+constexpr int waves_per_eu() {
+  return BM <= 32 ? 4 : (BM <= 64 ? 2 : 1);
+}
+
 template <int FMT, class AT, int BM, int NT, int GSM, bool MOE>
-__global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(waves_per_eu<BM>(), 8)))
+void marlin_gemm_kernel(const GemmParams p) {
   constexpr int MT = BM / 16;
   constexpr int BITS = fmt_bits(FMT);
   constexpr int BN = 4 * NT * 16;
@@ -97,7 +106,11 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
   constexpr int FRAGS = 4 * MT;            // A fragments per step
   static_assert(FRAGS % 4 == 0, "fragments split evenly over 4 waves");
 
-  __shared__ u32x4_t lds_a[2][FRAGS * 64];
+  // Two distinct LDS arrays (not one [2][...] array): the next step's global->LDS copies
+  // target the other array, and the compiler can only prove they do not alias the current
+  // step's ds_reads -- and so keep them in flight -- when the objects are distinct.
+  __shared__ u32x4_t lds_a0[FRAGS * 64];
+  __shared__ u32x4_t lds_a1[FRAGS * 64];
   __shared__ int lds_rows[BM];
   __shared__ int lds_last;
 
@@ -181,12 +194,13 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
   }
 
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
-  auto load_step = [&](int s, int buf, u32x4_t (&bw)[NT][NW], uint32_t (&raw)[NT][RAWB]) {
+  auto load_step = [&](int s, u32x4_t (&lds)[FRAGS * 64], u32x4_t (&bw)[NT][NW],
+                       MetaRaw (&raw)[NT][RAWB]) {
     // activations -> LDS
 #pragma unroll
     for (int i = 0; i < FPW; ++i) {
       const int f = wave + 4 * i;
-      lds_dma16(a_src[i] + s * 128, &lds_a[buf][f * 64]);
+      lds_dma16(a_src[i] + s * 128, &lds[f * 64]);
     }
     // weights
 #pragma unroll
@@ -215,11 +229,11 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
     }
   };
 
-  auto compute_block = [&](int buf, int b, const uint32_t w0[NT], const uint32_t w1[NT],
-                           const Meta (&mt_meta)[NT]) {
+  auto compute_block = [&](const u32x4_t (&lds)[FRAGS * 64], int b, const uint32_t w0[NT],
+                           const uint32_t w1[NT], const Meta (&mt_meta)[NT]) {
     u32x4_t af[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) af[i] = lds_a[buf][(b * MT + i) * 64 + lane];
+    for (int i = 0; i < MT; ++i) af[i] = lds[(b * MT + i) * 64 + lane];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const u32x4_t bop = dequant_operand<FMT, AT>(w0[t], w1[t], mt_meta[t]);
@@ -228,8 +242,8 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
     }
   };
 
-  auto compute_step = [&](int buf, const u32x4_t (&bw)[NT][NW], const uint32_t (&raw)[NT][RAWB],
-                          int nblocks) {
+  auto compute_step = [&](const u32x4_t (&lds)[FRAGS * 64], const u32x4_t (&bw)[NT][NW],
+                          const MetaRaw (&raw)[NT][RAWB], int nblocks) {
     Meta mm[NT];
     if constexpr (GSM == GSM_CHANNEL) {
 #pragma unroll
@@ -256,35 +270,34 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
             w1[t] = bw[t][b >> 1][(b & 1) * 2 + 1];
           }
         }
-        compute_block(buf, b, w0, w1, mm);
+        compute_block(lds, b, w0, w1, mm);
       }
     }
   };
 
-  // ---- main loop over full 128-deep steps -------------------------------------------------
-  int buf = 0;
+  // ---- main loop over full 128-deep steps, ping-pong between two register/LDS sets ------
   if (s_begin < s_end) {
-    u32x4_t bcur[NT][NW], bnext[NT][NW];
-    uint32_t rcur[NT][RAWB], rnext[NT][RAWB];
-    load_step(s_begin, 0, bcur, rcur);
+    u32x4_t b0[NT][NW], b1[NT][NW];
+    MetaRaw r0[NT][RAWB], r1[NT][RAWB];
+    load_step(s_begin, lds_a0, b0, r0);
     wait_vm_all();
     __syncthreads();
-    for (int s = s_begin; s < s_end; ++s) {
-      const bool more = s + 1 < s_end;
-      if (more) load_step(s + 1, buf ^ 1, bnext, rnext);
-      compute_step(buf, bcur, rcur, 4);
+    int s = s_begin;
+    while (true) {
+      bool more = s + 1 < s_end;
+      if (more) load_step(s + 1, lds_a1, b1, r1);
+      compute_step(lds_a0, b0, r0, 4);
       wait_vm_all();
       __syncthreads();
-      if (more) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-#pragma unroll
-          for (int w = 0; w < NW; ++w) bcur[t][w] = bnext[t][w];
-#pragma unroll
-          for (int r = 0; r < RAWB; ++r) rcur[t][r] = rnext[t][r];
-        }
-      }
-      buf ^= 1;
+      if (!more) break;
+      ++s;
+      more = s + 1 < s_end;
+      if (more) load_step(s + 1, lds_a0, b0, r0);
+      compute_step(lds_a1, b1, r1, 4);
+      wait_vm_all();
+      __syncthreads();
+      if (!more) break;
+      ++s;
     }
   }
 
@@ -296,10 +309,10 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
     for (int i = 0; i < FPW; ++i) {
       const int f = wave + 4 * i;
       const int b = f / MT;
-      if (b < nblocks) lds_dma16(a_src[i] + kt0, &lds_a[buf][f * 64]);
+      if (b < nblocks) lds_dma16(a_src[i] + kt0, &lds_a0[f * 64]);
     }
     u32x4_t bw[NT][NW];
-    uint32_t raw[NT][RAWB];
+    MetaRaw raw[NT][RAWB];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int64_t n = (int64_t)(tn0 + t) * 16 + ln;
@@ -324,12 +337,12 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
           raw[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, meta_base,
                                                           (kt0 + 32 * b + 8 * lg) >> p.group_shift,
                                                           (int)n)
-                                  : 0u;
+                                  : MetaRaw{0u, 0u};
       }
     }
     wait_vm_all();
     __syncthreads();
-    compute_step(buf, bw, raw, nblocks);
+    compute_step(lds_a0, bw, raw, nblocks);
   }
 
   // ---- epilogue --------------------------------------------------------------------------
@@ -387,16 +400,20 @@ __global__ __launch_bounds__(256) void marlin_gemm_kernel(const GemmParams p) {
           __hip_atomic_fetch_add(p.ws + orow * p.N + (tn0 + t) * 16 + ln, acc[i][t][e],
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-  __threadfence();
+  // Ordering without an agent-scope fence (which on gfx950 writes back and invalidates the
+  // whole L2): the partial sums are device-scope atomics performed at the memory side, so
+  // once they have completed (vmcnt drained) every later atomic on any XCD observes them.
+  // The arrival counter is bumped only after that, and the last arriver reads the sums with
+  // atomic exchanges, which cannot be served from a stale cache line.
+  wait_vm_all();
   __syncthreads();
   if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(p.counters + out_tile, 1, __ATOMIC_ACQ_REL,
+    const int prev = __hip_atomic_fetch_add(p.counters + out_tile, 1, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT);
     lds_last = (prev == p.splits - 1);
   }
   __syncthreads();
   if (!lds_last) return;
-  __threadfence();
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
