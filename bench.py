@@ -36,7 +36,24 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of config keys to run")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 256 MiB device copy (counter calibration for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_probe(steps: int) -> int:
+    """A plain copy of known size: 256 MiB read + 256 MiB written per launch."""
+    import torch
+
+    src = torch.randn(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": src.numel() * 4,
+                      "copy_probe_bytes_written": dst.numel() * 4, "launches": steps}))
+    return 0
 
 
 # ---------------------------------------------------------------------------------------
@@ -283,6 +300,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         return 1
+    if args.copy_probe:
+        return copy_probe(args.steps)
     from marlin_v100_amd import ops  # noqa: F401  (loads the native libraries; no fallback)
 
     only = set(filter(None, args.only.split(",")))
@@ -317,6 +336,14 @@ def main() -> int:
             print(f"# {key}: {configs[key]['layer_us']} us", file=sys.stderr, flush=True)
 
     t = head["us"] / 1e6
+    # HBM traffic per launch of the headline kernel, from the rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE runs (copy-kernel calibrated) recorded in profiles/ for this workload.
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                         "traffic_cfg2_m16.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("traffic_bytes")
     line = {
         "metric": METRIC,
         "value": head["weight_GBs"],
@@ -336,7 +363,7 @@ def main() -> int:
                    "cold_cache_rotation_copies": head["rotated_copies"]},
         "roofline": {"bound": "hbm", "achieved": head["alg_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["alg_GBs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic,
                      "kernel": "mmi::marlin_gemm_kernel<FMT_U4, BF16, 16, *, GSM_BIG, false>",
                      "algorithmic_bytes_per_launch": head["alg_bytes"]},
         "configs": configs,
