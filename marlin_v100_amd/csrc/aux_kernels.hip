@@ -20,10 +20,10 @@ __global__ void dequant_kernel(const GemmParams p, uint16_t* __restrict__ out, i
     const Meta m = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, 0, group, (int)n));
     uint32_t w0, w1 = 0;
     if constexpr (BITS == 4) {
-      w0 = p.b[layout_word_index(4, p.K, n, k0)];
+      w0 = p.b[layout_word_index(4, p.K, p.N, n, k0)];
     } else {
-      w0 = p.b[layout_word_index(8, p.K, n, k0)];
-      w1 = p.b[layout_word_index(8, p.K, n, k0 + 4)];
+      w0 = p.b[layout_word_index(8, p.K, p.N, n, k0)];
+      w1 = p.b[layout_word_index(8, p.K, p.N, n, k0 + 4)];
     }
     const u32x4_t v = dequant_operand<FMT, AT>(w0, w1, m);
     float alpha = 1.0f;

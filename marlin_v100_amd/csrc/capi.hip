@@ -157,7 +157,7 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
 
 // ---- tile selection -------------------------------------------------------------------
 struct Plan {
-  int bm, nt, splits, steps_per_split, n_blocks, m_blocks;
+  int bm, nt, ch, splits, steps_per_split, n_blocks, m_blocks, xcd_group_m;
 };
 
 int env_int(const char* name, int dflt) {
@@ -165,42 +165,49 @@ int env_int(const char* name, int dflt) {
   return (v && *v) ? atoi(v) : dflt;
 }
 
-// Dense selector.  Small M is weight-bandwidth bound: 16-row blocks, narrow column tiles
-// and split-K until the grid holds ~4 workgroups per CU.  Large M is MFMA bound: 128x256
-// blocks (each wave 128x64), split-K only when the grid cannot cover the CUs once.
+// Dense selector.
+//  * M <= 32 is weight-bandwidth bound: 16/32-row blocks, narrow column tiles (each wave one
+//    or two n16 tiles) and 2 KiB of weights per tile per K step, with split-K until the
+//    grid holds about 4 workgroups per CU so enough loads are in flight.
+//  * Larger M is MFMA bound: 64x256 or 128x256 blocks (each wave 64/128 x 64) visited in the
+//    XCD-aware grouped order; split-K only when the grid cannot cover the CUs once.
+// MARLIN_MI355X_TILE="bm,nt,ch" and MARLIN_MI355X_SPLIT_K override the choice (tuning).
 Plan select_dense(int64_t M, int64_t N, int64_t K, int cus) {
   Plan p{};
   if (M <= 16) {
     p.bm = 16;
-    p.nt = (N % 128 == 0 && N / 128 >= 2 * cus) ? 2 : 1;
-  } else if (M <= 32) {
+    p.nt = 1;
+    p.ch = 2;
+  } else if (M <= 32 && N % 128 == 0) {
     p.bm = 32;
-    p.nt = (N % 128 == 0) ? 2 : 1;
-    if (p.nt == 1) p.bm = 16;
-  } else if (M <= 64) {
+    p.nt = 2;
+    p.ch = 2;
+  } else if (M <= 64 && N % 256 == 0) {
     p.bm = 64;
     p.nt = 4;
-  } else {
+    p.ch = 1;
+  } else if (N % 256 == 0) {
     p.bm = 128;
     p.nt = 4;
-  }
-  if (N % (64 * p.nt) != 0) {
-    // fall back to the narrowest tile that divides N (N % 64 == 0 is guaranteed)
+    p.ch = 1;
+  } else {
+    p.bm = 16;  // narrowest tile that divides N (N % 64 == 0 is guaranteed)
     p.nt = 1;
-    if (p.bm > 32) p.bm = 32;
-    if (p.bm == 32) p.bm = 16;
+    p.ch = 2;
   }
-  // optional override for tuning: MARLIN_MI355X_TILE="bm,nt"
   if (const char* t = getenv("MARLIN_MI355X_TILE")) {
-    int bm = 0, nt = 0;
-    if (sscanf(t, "%d,%d", &bm, &nt) == 2) {
+    int bm = 0, nt = 0, ch = 1;
+    if (sscanf(t, "%d,%d,%d", &bm, &nt, &ch) >= 2) {
       p.bm = bm;
       p.nt = nt;
+      p.ch = ch;
     }
   }
   p.m_blocks = (int)((M + p.bm - 1) / p.bm);
   p.n_blocks = (int)(N / (64 * p.nt));
-  const int steps = (int)(K / 128);
+  p.xcd_group_m = p.bm >= 64 ? 4 : 0;
+  p.xcd_group_m = env_int("MARLIN_MI355X_XCD_GROUP_M", p.xcd_group_m);
+  const int steps = (int)(K / (128 * p.ch));
   const int64_t base = (int64_t)p.m_blocks * p.n_blocks;
   const int64_t target = (p.bm <= 32) ? (int64_t)cus * 4 : (int64_t)cus;
   int splits = 1;
@@ -451,6 +458,8 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     p.splits = plan.splits;
     p.steps_per_split = plan.steps_per_split;
     p.num_n_blocks = plan.n_blocks;
+    p.num_m_blocks = plan.m_blocks;
+    p.xcd_group_m = plan.xcd_group_m;
     if (plan.splits > 1) {
       Workspace& w = get_workspace(dev, s, (size_t)size_m * size_n,
                                    (size_t)plan.m_blocks * plan.n_blocks);
@@ -463,6 +472,7 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     l.gsm = mc.gsm;
     l.bm = plan.bm;
     l.nt = plan.nt;
+    l.ch = plan.ch;
     l.moe = false;
     l.grid = (unsigned)((int64_t)plan.m_blocks * plan.n_blocks * plan.splits);
     check_hip(dispatch_gemm(l, p, s), "marlin_gemm launch");
@@ -606,6 +616,8 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     p.splits = splits;
     p.steps_per_split = sps;
     p.num_n_blocks = n_blocks;
+    p.num_m_blocks = m_blocks;
+    p.xcd_group_m = 0;
     p.sorted_ids = sorted_token_ids;
     p.sorted_numel = (int)sorted_numel;
     p.expert_ids = expert_ids;
@@ -628,6 +640,7 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     l.gsm = mc.gsm;
     l.bm = bm;
     l.nt = nt;
+    l.ch = 1;
     l.moe = true;
     l.grid = (unsigned)((int64_t)m_blocks * n_blocks * splits);
     check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");

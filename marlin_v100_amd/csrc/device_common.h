@@ -1,22 +1,24 @@
 // device_common.h -- types, weight layout, dequant routines and MFMA wrappers for gfx950.
 //
-// Weight layout ("tile-chunk layout"), shared by the repack, dequant and GEMM kernels.
+// Weight layout ("chunk-major layout"), shared by the repack, dequant and GEMM kernels.
 // The packed weight buffer keeps the reference's container shape [K/16, N*16/pack] int32
 // (vllm/_custom_ops.py:1187-1193) but orders words for 64-wide wavefronts feeding
 // v_mfma_f32_16x16x32_{f16,bf16}:
-//   * Columns are split into n16 tiles; tile t owns a contiguous run of K*16/pack words.
-//   * Inside a tile, K is cut into chunks of 1 KiB = 64 lanes x 4 words.  A chunk covers
-//     KC = 128 k (4-bit) or KC = 64 k (8-bit).  Lane l of a wave owns column 16t + l%16 and
-//     lane-group g = l/16; its 4 words are consecutive, so one dwordx4 per lane loads the
-//     whole chunk with a fully coalesced 1 KiB wave access.
+//   * Columns are split into T = N/16 n16 tiles and K into chunks of KC = 128 k (4-bit) or
+//     KC = 64 k (8-bit).  One (tile, chunk) is 1 KiB = 64 lanes x 4 words.  Lane l owns
+//     column 16t + l%16 and lane-group g = l/16; its 4 words are consecutive, so one
+//     dwordx4 per lane loads the whole chunk with a fully coalesced 1 KiB wave access.
+//   * Chunks are stored chunk-major: chunk c of tile t sits at word (c*T + t) * 256.  At
+//     any K step every tile's chunk is adjacent, so all waves of the chip read one
+//     contiguous region instead of thousands of strided streams.
 //   * Word j of lane l holds, for 4-bit: the 8 values k = c*128 + 32*j + 8*g + [0..7]
 //     (k32 block j of the chunk); for 8-bit: the 4 values
 //     k = c*64 + 32*(j/2) + 8*g + 4*(j%2) + [0..3].  Values sit in natural order, value i in
 //     bits [i*bits, (i+1)*bits).
 //   * That is exactly the B operand of one 16x16x32 MFMA: lane l supplies column l%16 and
 //     k-slice 8*g..8*g+7 of a 32-deep block.  The A operand uses the same k-slice per lane.
-//   * K % KC != 0 leaves a tail of (K % KC)/32 k32 blocks per tile, stored after the full
-//     chunks with J = tail words per lane, lane-major.
+//   * K % KC != 0 leaves a tail of (K % KC)/32 k32 blocks per tile, stored after all full
+//     chunks, tile-major, J tail words per lane, lane-major.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -68,8 +70,9 @@ __host__ __device__ inline int64_t tile_words(int bits, int64_t size_k) {
 __host__ __device__ inline int chunk_k(int bits) { return bits == 4 ? 128 : 64; }
 
 // Word index of the word holding values (n, k..k+pack-1), k a multiple of pack.
-__host__ __device__ inline int64_t layout_word_index(int bits, int64_t size_k, int64_t n,
-                                                     int64_t k) {
+__host__ __device__ inline int64_t layout_word_index(int bits, int64_t size_k, int64_t size_n,
+                                                     int64_t n, int64_t k) {
+  const int64_t tiles = size_n >> 4;
   const int64_t t = n >> 4;
   const int64_t nl = n & 15;
   const int64_t kc = chunk_k(bits);
@@ -79,19 +82,10 @@ __host__ __device__ inline int64_t layout_word_index(int bits, int64_t size_k, i
   const int64_t blk = kin >> 5;    // k32 block inside chunk
   const int64_t g = (kin >> 3) & 3;
   const int64_t lane = g * 16 + nl;
-  int64_t j;
-  int64_t wpl;
-  if (bits == 4) {
-    j = blk;
-  } else {
-    j = blk * 2 + ((kin >> 2) & 1);
-  }
-  if (c < full) {
-    wpl = 4;
-  } else {
-    wpl = (size_k - full * kc) / 32 * (bits / 4);
-  }
-  return t * tile_words(bits, size_k) + c * 256 + lane * wpl + j;
+  const int64_t j = (bits == 4) ? blk : blk * 2 + ((kin >> 2) & 1);
+  if (c < full) return (c * tiles + t) * 256 + lane * 4 + j;
+  const int64_t wpl = (size_k - full * kc) / 32 * (bits / 4);  // tail words per lane
+  return full * tiles * 256 + (t * 64 + lane) * wpl + j;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -199,6 +193,14 @@ __device__ __forceinline__ Meta make_meta(MetaRaw raw) {
   return m;
 }
 
+// (x & mask) | bits in one VALU op.  VOP3 on gfx9 takes no literal operands, so the compiler
+// would otherwise emit v_and_b32 + v_or_b32; the constants live in registers instead.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "s"(bits));
+  return r;
+}
+
 __device__ __forceinline__ float h_lo(uint32_t x) {
   return (float)__builtin_bit_cast(f16x2_t, x)[0];
 }
@@ -212,11 +214,11 @@ template <int FMT, class AT>
 __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, const Meta& m) {
   u32x4_t r;
   if constexpr (FMT == FMT_U4B8 || FMT == FMT_U4) {
-    const uint32_t x0 = (w0 & 0x000f000fu) | 0x64006400u;  // k0, k4  : 1024 + q
-    const uint32_t x1 = (w0 & 0x00f000f0u) | 0x64006400u;  // k1, k5  : 1024 + 16q
+    const uint32_t x0 = and_or(w0, 0x000f000fu, 0x64006400u);  // k0, k4  : 1024 + q
+    const uint32_t x1 = and_or(w0, 0x00f000f0u, 0x64006400u);  // k1, k5  : 1024 + 16q
     const uint32_t t = w0 >> 8;
-    const uint32_t x2 = (t & 0x000f000fu) | 0x64006400u;  // k2, k6
-    const uint32_t x3 = (t & 0x00f000f0u) | 0x64006400u;  // k3, k7
+    const uint32_t x2 = and_or(t, 0x000f000fu, 0x64006400u);  // k2, k6
+    const uint32_t x3 = and_or(t, 0x00f000f0u, 0x64006400u);  // k3, k7
     const float e0 = __builtin_fmaf(h_lo(x0), m.s, m.c1);
     const float e4 = __builtin_fmaf(h_hi(x0), m.s, m.c1);
     const float e1 = __builtin_fmaf(h_lo(x1), m.s16, m.c16);
@@ -230,10 +232,10 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
     r[2] = pack2(e4, e5, AT{});
     r[3] = pack2(e6, e7, AT{});
   } else if constexpr (FMT == FMT_U8B128 || FMT == FMT_U8) {
-    const uint32_t a0 = (w0 & 0x00ff00ffu) | 0x64006400u;         // k0, k2
-    const uint32_t a1 = ((w0 >> 8) & 0x00ff00ffu) | 0x64006400u;  // k1, k3
-    const uint32_t b0 = (w1 & 0x00ff00ffu) | 0x64006400u;         // k4, k6
-    const uint32_t b1 = ((w1 >> 8) & 0x00ff00ffu) | 0x64006400u;  // k5, k7
+    const uint32_t a0 = and_or(w0, 0x00ff00ffu, 0x64006400u);       // k0, k2
+    const uint32_t a1 = and_or(w0 >> 8, 0x00ff00ffu, 0x64006400u);  // k1, k3
+    const uint32_t b0 = and_or(w1, 0x00ff00ffu, 0x64006400u);       // k4, k6
+    const uint32_t b1 = and_or(w1 >> 8, 0x00ff00ffu, 0x64006400u);  // k5, k7
     r[0] = pack2(__builtin_fmaf(h_lo(a0), m.s, m.c1), __builtin_fmaf(h_lo(a1), m.s, m.c1),
                  AT{});
     r[1] = pack2(__builtin_fmaf(h_hi(a0), m.s, m.c1), __builtin_fmaf(h_hi(a1), m.s, m.c1),

@@ -8,23 +8,24 @@ namespace mmi {
 template <int FMT, class AT, int GSM>
 static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
   const dim3 grid(l.grid), block(256);
-#define MMI_CASE(BM_, NT_, MOE_)                                                               \
-  if (l.bm == BM_ && l.nt == NT_ && l.moe == MOE_) {                                           \
-    hipLaunchKernelGGL((marlin_gemm_kernel<FMT, AT, BM_, NT_, GSM, MOE_>), grid, block, 0, s, p); \
+#define MMI_CASE(BM_, NT_, CH_, MOE_)                                                          \
+  if (l.bm == BM_ && l.nt == NT_ && l.ch == CH_ && l.moe == MOE_) {                            \
+    hipLaunchKernelGGL((marlin_gemm_kernel<FMT, AT, BM_, NT_, CH_, GSM, MOE_>), grid, block, 0, \
+                       s, p);                                                                  \
     return hipGetLastError();                                                                  \
   }
-  // dense
-  MMI_CASE(16, 1, false)
-  MMI_CASE(16, 2, false)
-  MMI_CASE(16, 4, false)
-  MMI_CASE(32, 2, false)
-  MMI_CASE(64, 4, false)
-  MMI_CASE(128, 4, false)
+  // dense: small-M weight streaming tiles, then MFMA tiles
+  MMI_CASE(16, 1, 1, false)
+  MMI_CASE(16, 1, 2, false)
+  MMI_CASE(16, 2, 2, false)
+  MMI_CASE(32, 2, 2, false)
+  MMI_CASE(64, 4, 1, false)
+  MMI_CASE(128, 4, 1, false)
   // MoE: one moe block per workgroup
-  MMI_CASE(16, 4, true)
-  MMI_CASE(32, 4, true)
-  MMI_CASE(48, 4, true)
-  MMI_CASE(64, 4, true)
+  MMI_CASE(16, 4, 1, true)
+  MMI_CASE(32, 4, 1, true)
+  MMI_CASE(48, 4, 1, true)
+  MMI_CASE(64, 4, 1, true)
 #undef MMI_CASE
   return hipErrorInvalidValue;
 }

@@ -4,17 +4,20 @@
 //   * a workgroup owns a BM x BN output block, BN = 4 waves x NT n16-tiles x 16 columns;
 //     all four waves share the BM activation rows and own disjoint columns, so no weight
 //     is dequantized twice;
-//   * K advances in steps of 128.  Activation rows for the step are copied straight into LDS
-//     with global_load_lds_dwordx4 (no VGPR staging), laid out fragment-major so every
-//     ds_read_b128 of an MFMA A operand is conflict-free;
-//   * weights never touch LDS: each lane loads its dwordx4 of the tile-chunk layout
+//   * K advances in steps of CH chunks (128*CH deep).  Activation rows for the step are
+//     copied straight into LDS with global_load_lds_dwordx4 (no VGPR staging), laid out
+//     fragment-major so every ds_read_b128 of an MFMA A operand is conflict-free;
+//   * weights never touch LDS: each lane loads its dwordx4s of the chunk-major layout
 //     (device_common.h), dequantizes in registers and feeds v_mfma_f32_16x16x32;
-//   * the next step's activations (LDS, double buffered), weights and scale metadata are
-//     in flight while the current step computes;
+//   * the next step's activations, weights and scale metadata are in flight while the
+//     current step computes (two LDS arrays / register sets, loop unrolled by two);
 //   * split-K partitions the K steps; partial sums go to an fp32 workspace with device-scope
 //     atomics, the last workgroup to finish an output block (per-block arrival counter)
 //     applies the epilogue and resets its workspace slice and counter to zero, so the
-//     workspace needs no clearing between calls.
+//     workspace needs no clearing between calls;
+//   * dense tiles are visited in an XCD-aware grouped order: consecutive workgroup ids go
+//     to different XCDs, so ids are remapped such that each XCD works on a compact group
+//     of output tiles and reuses the activation and weight slabs from its own L2.
 // MoE (reference sm70_marlin_gemm.cuh:3591-3686): a workgroup's rows are one moe block of
 // expert-sorted route ids; A rows are gathered as id / top_k, C rows scattered to id.
 #pragma once
@@ -40,6 +43,8 @@ struct GemmParams {
   int splits;
   int steps_per_split;
   int num_n_blocks;
+  int num_m_blocks;
+  int xcd_group_m;  // m-blocks per group in the XCD-aware order (0: plain order)
   float* ws;
   int* counters;
   // MoE
@@ -57,6 +62,8 @@ struct GemmParams {
 
 // Group-size modes.
 enum { GSM_CHANNEL = 0, GSM_BIG = 1, GSM_SMALL = 2 };
+
+constexpr int kNumXcd = 8;
 
 template <class AT>
 __device__ __forceinline__ uint32_t load_u16(const void* p, int64_t idx) {
@@ -88,6 +95,36 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, void* lds_wave_base)
 
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Workgroup id -> (split, n block, m block).  Dense launches use the XCD-aware grouped
+// order when p.xcd_group_m > 0; MoE launches keep the plain order (one moe block per row).
+__device__ __forceinline__ void decode_block(const GemmParams& p, int& split, int& n_blk,
+                                             int& m_blk) {
+  int id = blockIdx.x;
+  const int total = gridDim.x;
+  if (p.xcd_group_m > 0) {
+    const int full = total - total % kNumXcd;
+    if (id < full) {
+      const int per = full / kNumXcd;
+      id = (id % kNumXcd) * per + id / kNumXcd;
+    }
+  }
+  split = id % p.splits;
+  const int tile = id / p.splits;
+  if (p.xcd_group_m > 0) {
+    const int gm_full = p.xcd_group_m;
+    const int per_group = gm_full * p.num_n_blocks;
+    const int g = tile / per_group;
+    const int first_m = g * gm_full;
+    const int gm = min(p.num_m_blocks - first_m, gm_full);
+    const int in = tile - g * per_group;
+    m_blk = first_m + in % gm;
+    n_blk = in / gm;
+  } else {
+    n_blk = tile % p.num_n_blocks;
+    m_blk = tile / p.num_n_blocks;
+  }
+}
+
 // Waves per SIMD the register allocation must leave room for: the small-M (weight
 // streaming) tiles need many waves in flight, the 128-row tiles trade occupancy for
 // accumulators.
@@ -96,15 +133,19 @@ constexpr int waves_per_eu() {
   return BM <= 32 ? 4 : (BM <= 64 ? 2 : 1);
 }
 
-template <int FMT, class AT, int BM, int NT, int GSM, bool MOE>
+template <int FMT, class AT, int BM, int NT, int CH, int GSM, bool MOE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(waves_per_eu<BM>(), 8)))
 void marlin_gemm_kernel(const GemmParams p) {
   constexpr int MT = BM / 16;
   constexpr int BITS = fmt_bits(FMT);
   constexpr int BN = 4 * NT * 16;
-  constexpr int NW = (BITS == 4) ? 1 : 2;  // uint4 loads per tile per full step
-  constexpr int FRAGS = 4 * MT;            // A fragments per step
+  constexpr int NB = 4 * CH;                      // k32 blocks per step
+  constexpr int KS = 128 * CH;                    // k per step
+  constexpr int NL = (BITS == 4) ? CH : 2 * CH;   // 1 KiB chunk loads per tile per step
+  constexpr int FRAGS = NB * MT;                  // A fragments per step
+  constexpr int FPW = FRAGS / 4;                  // A fragments copied by each wave
   static_assert(FRAGS % 4 == 0, "fragments split evenly over 4 waves");
+  constexpr int RAWB = (GSM == GSM_SMALL) ? NB : (GSM == GSM_BIG ? CH : 1);
 
   // Two distinct LDS arrays (not one [2][...] array): the next step's global->LDS copies
   // target the other array, and the compiler can only prove they do not alias the current
@@ -117,15 +158,12 @@ void marlin_gemm_kernel(const GemmParams p) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int lg = lane >> 4;   // lane group: k-slice 8*lg inside a 32-deep block
-  const int ln = lane & 15;   // column (B) / row (A) inside a 16-wide fragment
+  const int lg = lane >> 4;  // lane group: k-slice 8*lg inside a 32-deep block
+  const int ln = lane & 15;  // column (B) / row (A) inside a 16-wide fragment
 
-  int bid = blockIdx.x;
-  const int split = bid % p.splits;
-  bid /= p.splits;
-  const int n_blk = bid % p.num_n_blocks;
-  const int m_blk = bid / p.num_n_blocks;
-  const int out_tile = bid;
+  int split, n_blk, m_blk;
+  decode_block(p, split, n_blk, m_blk);
+  const int out_tile = m_blk * p.num_n_blocks + n_blk;
 
   int expert = 0;
   // activations as raw 16-bit words (AT is a tag type, not the element type)
@@ -149,7 +187,7 @@ void marlin_gemm_kernel(const GemmParams p) {
   const int m0 = MOE ? 0 : m_blk * BM;
 
   // ---- activation rows this wave copies into LDS: fragments f = wave + 4*i --------------
-  constexpr int FPW = FRAGS / 4;  // fragments per wave per step
+  // fragment f covers k32 block f / MT and m16 tile f % MT of the step
   const uint16_t* a_src[FPW];
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
@@ -169,12 +207,13 @@ void marlin_gemm_kernel(const GemmParams p) {
 
   // ---- weight / metadata addressing ------------------------------------------------------
   const int tn0 = n_blk * (BN / 16) + wave * NT;  // first n16 tile of this wave
-  const int64_t twords = tile_words(BITS, p.K);
-  const uint32_t* bptr = p.b + (int64_t)expert * p.b_expert_stride + (int64_t)tn0 * twords;
+  // chunk c of tile t is at word (c * tiles + t) * 256 (chunk-major layout)
+  const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
+  const uint32_t* bptr = p.b + (int64_t)expert * p.b_expert_stride + (int64_t)tn0 * 256 + lane * 4;
   const int64_t meta_base = (int64_t)expert * p.meta_expert_stride;
 
-  const int total_full = p.K / 128;
-  const int k_tail = p.K - total_full * 128;
+  const int total_full = p.K / KS;
+  const int k_tail = p.K - total_full * KS;
   const int s_begin = split * p.steps_per_split;
   const int s_end = min(total_full, s_begin + p.steps_per_split);
   const bool do_tail = (k_tail != 0) && (split == p.splits - 1);
@@ -193,91 +232,84 @@ void marlin_gemm_kernel(const GemmParams p) {
       meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
   }
 
-  constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
-  auto load_step = [&](int s, u32x4_t (&lds)[FRAGS * 64], u32x4_t (&bw)[NT][NW],
+  auto load_step = [&](int s, u32x4_t (&lds)[FRAGS * 64], u32x4_t (&bw)[NT][NL],
                        MetaRaw (&raw)[NT][RAWB]) {
+    const int k0 = s * KS;
     // activations -> LDS
 #pragma unroll
     for (int i = 0; i < FPW; ++i) {
       const int f = wave + 4 * i;
-      lds_dma16(a_src[i] + s * 128, &lds[f * 64]);
+      lds_dma16(a_src[i] + k0, &lds[f * 64]);
     }
-    // weights
+    // weights: NL consecutive 1 KiB chunks of each tile
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const uint32_t* tp = bptr + t * twords + lane * 4;
-      if constexpr (BITS == 4) {
-        bw[t][0] = *reinterpret_cast<const u32x4_t*>(tp + (int64_t)s * 256);
-      } else {
-        bw[t][0] = *reinterpret_cast<const u32x4_t*>(tp + (int64_t)(2 * s) * 256);
-        bw[t][1] = *reinterpret_cast<const u32x4_t*>(tp + (int64_t)(2 * s + 1) * 256);
-      }
+      const uint32_t* tp = bptr + t * 256 + (int64_t)s * NL * chunk_stride;
+#pragma unroll
+      for (int c = 0; c < NL; ++c)
+        bw[t][c] = *reinterpret_cast<const u32x4_t*>(tp + c * chunk_stride);
     }
     // metadata
     if constexpr (GSM == GSM_BIG) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        raw[t][0] = load_meta_raw<FMT, AT>(p, meta_base, (s * 128) >> p.group_shift,
-                                           (tn0 + t) * 16 + ln);
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+          raw[t][c] = load_meta_raw<FMT, AT>(p, meta_base, (k0 + 128 * c) >> p.group_shift,
+                                             (tn0 + t) * 16 + ln);
     } else if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-          raw[t][b] = load_meta_raw<FMT, AT>(p, meta_base, (s * 128 + 32 * b + 8 * lg) >> p.group_shift,
+        for (int b = 0; b < NB; ++b)
+          raw[t][b] = load_meta_raw<FMT, AT>(p, meta_base, (k0 + 32 * b + 8 * lg) >> p.group_shift,
                                              (tn0 + t) * 16 + ln);
     }
   };
 
-  auto compute_block = [&](const u32x4_t (&lds)[FRAGS * 64], int b, const uint32_t w0[NT],
-                           const uint32_t w1[NT], const Meta (&mt_meta)[NT]) {
-    u32x4_t af[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) af[i] = lds[(b * MT + i) * 64 + lane];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const u32x4_t bop = dequant_operand<FMT, AT>(w0[t], w1[t], mt_meta[t]);
-#pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i][t] = mfma16(af[i], bop, acc[i][t], AT{});
-    }
-  };
-
-  auto compute_step = [&](const u32x4_t (&lds)[FRAGS * 64], const u32x4_t (&bw)[NT][NW],
+  auto compute_step = [&](const u32x4_t (&lds)[FRAGS * 64], const u32x4_t (&bw)[NT][NL],
                           const MetaRaw (&raw)[NT][RAWB], int nblocks) {
     Meta mm[NT];
     if constexpr (GSM == GSM_CHANNEL) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) mm[t] = meta_ch[t];
-    } else if constexpr (GSM == GSM_BIG) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(raw[t][0]);
     }
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < NB; ++b) {
       if (b < nblocks) {
         if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
           for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(raw[t][b]);
-        }
-        uint32_t w0[NT], w1[NT];
+        } else if constexpr (GSM == GSM_BIG) {
+          if ((b & 3) == 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          if constexpr (BITS == 4) {
-            w0[t] = bw[t][0][b];
-            w1[t] = 0;
-          } else {
-            w0[t] = bw[t][b >> 1][(b & 1) * 2];
-            w1[t] = bw[t][b >> 1][(b & 1) * 2 + 1];
+            for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(raw[t][b >> 2]);
           }
         }
-        compute_block(lds, b, w0, w1, mm);
+        u32x4_t af[MT];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) af[i] = lds[(b * MT + i) * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          uint32_t w0, w1;
+          if constexpr (BITS == 4) {
+            w0 = bw[t][b >> 2][b & 3];
+            w1 = 0;
+          } else {
+            w0 = bw[t][b >> 1][(b & 1) * 2];
+            w1 = bw[t][b >> 1][(b & 1) * 2 + 1];
+          }
+          const u32x4_t bop = dequant_operand<FMT, AT>(w0, w1, mm[t]);
+#pragma unroll
+          for (int i = 0; i < MT; ++i) acc[i][t] = mfma16(af[i], bop, acc[i][t], AT{});
+        }
       }
     }
   };
 
-  // ---- main loop over full 128-deep steps, ping-pong between two register/LDS sets ------
+  // ---- main loop over full steps, ping-pong between two register / LDS sets ---------------
   if (s_begin < s_end) {
-    u32x4_t b0[NT][NW], b1[NT][NW];
+    u32x4_t b0[NT][NL], b1[NT][NL];
     MetaRaw r0[NT][RAWB], r1[NT][RAWB];
     load_step(s_begin, lds_a0, b0, r0);
     wait_vm_all();
@@ -286,14 +318,14 @@ void marlin_gemm_kernel(const GemmParams p) {
     while (true) {
       bool more = s + 1 < s_end;
       if (more) load_step(s + 1, lds_a1, b1, r1);
-      compute_step(lds_a0, b0, r0, 4);
+      compute_step(lds_a0, b0, r0, NB);
       wait_vm_all();
       __syncthreads();
       if (!more) break;
       ++s;
       more = s + 1 < s_end;
       if (more) load_step(s + 1, lds_a0, b0, r0);
-      compute_step(lds_a1, b1, r1, 4);
+      compute_step(lds_a1, b1, r1, NB);
       wait_vm_all();
       __syncthreads();
       if (!more) break;
@@ -301,39 +333,44 @@ void marlin_gemm_kernel(const GemmParams p) {
     }
   }
 
-  // ---- K tail: (K % 128) / 32 blocks, read word by word through the layout map -----------
+  // ---- K tail: (K % KS) / 32 blocks, read word by word through the layout map ------------
   if (do_tail) {
     const int nblocks = k_tail / 32;
-    const int kt0 = total_full * 128;
+    const int kt0 = total_full * KS;
 #pragma unroll
     for (int i = 0; i < FPW; ++i) {
       const int f = wave + 4 * i;
       const int b = f / MT;
       if (b < nblocks) lds_dma16(a_src[i] + kt0, &lds_a0[f * 64]);
     }
-    u32x4_t bw[NT][NW];
+    u32x4_t bw[NT][NL];
     MetaRaw raw[NT][RAWB];
+    const uint32_t* base = p.b + (int64_t)expert * p.b_expert_stride;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int64_t n = (int64_t)(tn0 + t) * 16 + ln;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < NB; ++b) {
         if (b < nblocks) {
           const int64_t k = kt0 + 32 * b + 8 * lg;
-          const uint32_t* base = p.b + (int64_t)expert * p.b_expert_stride;
           if constexpr (BITS == 4) {
-            bw[t][0][b] = base[layout_word_index(4, p.K, n, k)];
+            bw[t][b >> 2][b & 3] = base[layout_word_index(4, p.K, p.N, n, k)];
           } else {
-            bw[t][b >> 1][(b & 1) * 2] = base[layout_word_index(8, p.K, n, k)];
-            bw[t][b >> 1][(b & 1) * 2 + 1] = base[layout_word_index(8, p.K, n, k + 4)];
+            bw[t][b >> 1][(b & 1) * 2] = base[layout_word_index(8, p.K, p.N, n, k)];
+            bw[t][b >> 1][(b & 1) * 2 + 1] = base[layout_word_index(8, p.K, p.N, n, k + 4)];
           }
         }
       }
       if constexpr (GSM == GSM_BIG) {
-        raw[t][0] = load_meta_raw<FMT, AT>(p, meta_base, kt0 >> p.group_shift, (int)n);
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+          raw[t][c] = 4 * c < nblocks ? load_meta_raw<FMT, AT>(p, meta_base,
+                                                              (kt0 + 128 * c) >> p.group_shift,
+                                                              (int)n)
+                                      : MetaRaw{0u, 0u};
       } else if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < NB; ++b)
           raw[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, meta_base,
                                                           (kt0 + 32 * b + 8 * lg) >> p.group_shift,
                                                           (int)n)

@@ -30,6 +30,7 @@ struct GemmLaunch {
   int gsm;   // GSM_CHANNEL / GSM_BIG / GSM_SMALL
   int bm;    // rows per workgroup
   int nt;    // n16 tiles per wave
+  int ch;    // 1 KiB weight chunks per tile per K step
   bool moe;
   unsigned grid;
 };

@@ -11,26 +11,29 @@
 
 namespace mmi {
 
-// Decode an output word index into (n, k of its first value).
-__device__ __forceinline__ void decode_word(int bits, int64_t size_k, int64_t w, int64_t& n,
-                                            int64_t& k) {
-  const int64_t tw = tile_words(bits, size_k);
-  const int64_t t = w / tw;
-  int64_t r = w - t * tw;
+// Decode an output word index into (n, k of its first value); inverse of
+// layout_word_index().
+__device__ __forceinline__ void decode_word(int bits, int64_t size_k, int64_t size_n, int64_t w,
+                                            int64_t& n, int64_t& k) {
+  const int64_t tiles = size_n >> 4;
   const int64_t kc = chunk_k(bits);
   const int64_t full = size_k / kc;
-  int64_t c = r / 256;
-  int64_t lane, j;
-  if (c < full) {
-    r -= c * 256;
-    lane = r >> 2;
-    j = r & 3;
+  const int64_t full_words = full * tiles * 256;
+  int64_t t, c, lane, j;
+  if (w < full_words) {
+    const int64_t chunk = w >> 8;
+    c = chunk / tiles;
+    t = chunk - c * tiles;
+    lane = (w >> 2) & 63;
+    j = w & 3;
   } else {
-    c = full;
-    r -= full * 256;
     const int64_t wpl = (size_k - full * kc) / 32 * (bits / 4);
-    lane = r / wpl;
-    j = r - lane * wpl;
+    const int64_t r = w - full_words;
+    const int64_t tl = r / wpl;  // t * 64 + lane
+    j = r - tl * wpl;
+    t = tl >> 6;
+    lane = tl & 63;
+    c = full;
   }
   const int64_t g = lane >> 4;
   n = t * 16 + (lane & 15);
@@ -50,7 +53,7 @@ __global__ void gptq_repack_kernel(const uint32_t* __restrict__ src, const int* 
   for (int64_t w = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; w < total_words;
        w += (int64_t)gridDim.x * blockDim.x) {
     int64_t n, k;
-    decode_word(BITS, size_k, w, n, k);
+    decode_word(BITS, size_k, size_n, w, n, k);
     uint32_t v;
     if constexpr (!HAS_PERM) {
       v = src[(k / PACK) * size_n + n];
@@ -77,7 +80,7 @@ __global__ void awq_repack_kernel(const uint32_t* __restrict__ src, uint32_t* __
   for (int64_t w = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; w < total_words;
        w += (int64_t)gridDim.x * blockDim.x) {
     int64_t n, k;
-    decode_word(BITS, size_k, w, n, k);
+    decode_word(BITS, size_k, size_n, w, n, k);
     const int c = (int)(n % PACK);
     int slot;
     if constexpr (BITS == 4) {
