@@ -25,7 +25,7 @@ __global__ void dequant_kernel(const GemmParams p, uint16_t* __restrict__ out, i
       w0 = p.b[layout_word_index(8, p.K, p.N, n, k0)];
       w1 = p.b[layout_word_index(8, p.K, p.N, n, k0 + 4)];
     }
-    const u32x4_t v = dequant_operand<FMT, AT>(w0, w1, m);
+    const u32x4_t v = dequant_operand<FMT, AT>(w0, w1, m, opaque_zero(p.zero));
     float alpha = 1.0f;
     if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[0], p.alpha_exp);
 #pragma unroll

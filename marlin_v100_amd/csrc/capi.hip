@@ -10,6 +10,7 @@
 #include <mutex>
 #include <sstream>
 #include <string>
+#include <tuple>
 #include <utility>
 
 #include "../../include/marlin_mi355x.h"
@@ -157,8 +158,29 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
 
 // ---- tile selection -------------------------------------------------------------------
 struct Plan {
-  int bm, nt, ch, splits, steps_per_split, n_blocks, m_blocks, xcd_group_m;
+  int bm, nt, ch, depth, wpb, ksplit, splits, steps_per_split, n_blocks, m_blocks, xcd_group_m;
+  int64_t grid;
 };
+
+hipError_t dispatch_gemm(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+
+// Workgroups of one kernel instance that fit on a CU at once (cached per instance).
+int blocks_per_cu(const GemmLaunch& l) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int>, int> cache;
+  const auto key = std::make_tuple(l.fmt, (int)l.bf16, l.gsm, l.bm, l.nt, l.ch, l.depth, l.wpb,
+                                   (int)l.ksplit, (int)l.moe);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  GemmLaunch q = l;
+  int occ = 0;
+  q.occupancy = &occ;
+  GemmParams dummy{};
+  if (dispatch_gemm(q, dummy, nullptr) != hipSuccess || occ < 1) occ = 1;
+  cache.emplace(key, occ);
+  return occ;
+}
 
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
@@ -166,14 +188,61 @@ int env_int(const char* name, int dflt) {
 }
 
 // Dense selector.
-//  * M <= 32 is weight-bandwidth bound: 16/32-row blocks, narrow column tiles (each wave one
-//    or two n16 tiles) and 2 KiB of weights per tile per K step, with split-K until the
-//    grid holds about 4 workgroups per CU so enough loads are in flight.
+//  * M <= 16 (decode) is weight-bandwidth bound: the decode kernel, each wave NT n16 tiles,
+//    loads DEPTH-1 K steps ahead, WPB waves per workgroup on adjacent columns.  All of its
+//    workgroups must be resident at once -- a second, partial round of workgroups would
+//    stream its weights alone at the end -- so K is split across workgroups only as far as
+//    the grid still fits on the chip in one round.
+//  * 16 < M <= 32 is still weight bound: 32-row blocks with split-K until the grid holds
+//    about 4 workgroups per CU.
 //  * Larger M is MFMA bound: 64x256 or 128x256 blocks (each wave 64/128 x 64) visited in the
 //    XCD-aware grouped order; split-K only when the grid cannot cover the CUs once.
+// MARLIN_MI355X_DECODE="nt,depth,wpb" (nt 0 disables the decode kernel),
 // MARLIN_MI355X_TILE="bm,nt,ch" and MARLIN_MI355X_SPLIT_K override the choice (tuning).
-Plan select_dense(int64_t M, int64_t N, int64_t K, int cus) {
+Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& kinds) {
   Plan p{};
+  // The decode kernel pays off where it multiplies raw codes (integer-operand path: integer
+  // and fp8 weights with channelwise or >= 128-deep groups); fp4 weights and small groups
+  // dequantize per weight and stay on the tiled kernel.
+  const bool int_operand = kinds.fmt != FMT_MXFP4 && kinds.fmt != FMT_NVFP4 && kinds.gsm != GSM_SMALL;
+  if (M <= 16 && (int_operand || getenv("MARLIN_MI355X_DECODE") != nullptr)) {
+    int nt = 4, depth = 3, wpb = 4, ksplit = 1;
+    if (const char* t = getenv("MARLIN_MI355X_DECODE"))
+      sscanf(t, "%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit);
+    if (nt > 0 && N % (16 * nt) == 0) {
+      const int64_t groups = N / (16 * nt);
+      while (!ksplit && wpb > 1 && groups % wpb != 0) wpb /= 2;
+      p.bm = 16;
+      p.nt = nt;
+      p.ch = 1;
+      p.depth = depth;
+      p.wpb = wpb;
+      p.ksplit = ksplit;
+      p.m_blocks = 1;
+      p.n_blocks = (int)groups;  // split-K counters are per column group
+      p.xcd_group_m = 0;
+      GemmLaunch q = kinds;
+      q.bm = p.bm;
+      q.nt = nt;
+      q.ch = 1;
+      q.depth = depth;
+      q.wpb = wpb;
+      q.ksplit = ksplit != 0;
+      const int64_t resident = (int64_t)blocks_per_cu(q) * cus;
+      const int64_t blocks_n = ksplit ? groups : groups / wpb;
+      const int steps = (int)(K / 128);
+      int splits = 1;
+      const int min_steps = 2 * (ksplit ? wpb : 1);  // per split
+      if (blocks_n < resident && steps >= 2 * min_steps)
+        splits = (int)std::min<int64_t>(resident / blocks_n, steps / min_steps);
+      splits = env_int("MARLIN_MI355X_SPLIT_K", splits);
+      splits = std::max(1, std::min(splits, std::max(steps, 1)));
+      p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
+      p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
+      p.grid = blocks_n * p.splits;
+      return p;
+    }
+  }
   if (M <= 16) {
     p.bm = 16;
     p.nt = 1;
@@ -221,6 +290,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus) {
   splits = std::max(1, std::min(splits, std::max(steps, 1)));
   p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
   p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
+  p.grid = (int64_t)p.m_blocks * p.n_blocks * p.splits;
   return p;
 }
 
@@ -437,7 +507,11 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     hipStream_t s = (hipStream_t)stream;
     int dev = 0;
     check_hip(hipGetDevice(&dev), "hipGetDevice");
-    const Plan plan = select_dense(size_m, size_n, size_k, device_cu_count(dev));
+    GemmLaunch l{};
+    l.fmt = mc.fmt;
+    l.bf16 = a_dtype == MARLIN_DTYPE_BFLOAT16;
+    l.gsm = mc.gsm;
+    const Plan plan = select_dense(size_m, size_n, size_k, device_cu_count(dev), l);
 
     GemmParams p{};
     p.a = a;
@@ -466,15 +540,14 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
       p.ws = w.ws;
       p.counters = w.counters;
     }
-    GemmLaunch l{};
-    l.fmt = mc.fmt;
-    l.bf16 = a_dtype == MARLIN_DTYPE_BFLOAT16;
-    l.gsm = mc.gsm;
     l.bm = plan.bm;
     l.nt = plan.nt;
     l.ch = plan.ch;
+    l.depth = plan.depth;
+    l.wpb = plan.wpb;
+    l.ksplit = plan.ksplit != 0;
     l.moe = false;
-    l.grid = (unsigned)((int64_t)plan.m_blocks * plan.n_blocks * plan.splits);
+    l.grid = (unsigned)plan.grid;
     check_hip(dispatch_gemm(l, p, s), "marlin_gemm launch");
   });
 }

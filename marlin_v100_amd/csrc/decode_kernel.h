@@ -1,0 +1,360 @@
+// decode_kernel.h -- weight-streaming GEMM for M <= 16 (decode), gfx950.
+//
+// At M <= 16 the GEMM is bound by streaming the packed weights from HBM, and the kernel's
+// job is to keep enough weight bytes in flight on every CU without ever making waves wait
+// on each other inside the K loop:
+//   * each wave owns NT n16 tiles (16*NT columns) and a range of K steps (128 deep).  The
+//     WPB waves of a workgroup either split the K range of one column group (KSPLIT: their
+//     partial sums are added through LDS once at the end, no global atomics) or own
+//     adjacent column groups over the same K range (they then read the same activation
+//     slices at about the same time and share them through the CU's L1 cache);
+//   * per step each lane loads one dwordx4 of the chunk-major weight layout
+//     (device_common.h) per tile, its activation slice (8 values of row l%16; rows >= M
+//     read row M-1) and the step's scale metadata into a register ring of DEPTH slots, so
+//     DEPTH-1 steps are in flight while one is multiplied.  (A ring in LDS, filled by
+//     global_load_lds_dwordx4, would save the registers, but the compiler's wait-count
+//     insertion does not tell the slots of such a ring apart and waits for every pending
+//     copy before each LDS read, which serializes the pipeline.);
+//   * slots are compile-time indices (static_for), the loop body is branch-free, so the
+//     compiler's vmcnt bookkeeping sees the same pending loads on every trip and waits only
+//     for the step it consumes;
+//   * integer and fp8 weights use the integer-operand path (device_common.h): the MFMA B
+//     operand is the code itself and the scale / zero point is applied per group to the
+//     fp32 partial sums;
+//   * split-K across workgroups, when the grid needs it, and the epilogue are those of the
+//     tiled kernel (fp32 workspace, arrival counters, last arriver finishes).
+#pragma once
+
+#include <type_traits>
+
+#include "gemm_kernel.h"
+
+namespace mmi {
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>), fully unrolled.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
+template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM>
+__global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParams p) {
+  constexpr int BITS = fmt_bits(FMT);
+  constexpr int NL = (BITS == 4) ? 1 : 2;  // 1 KiB chunks per tile per 128-deep step
+  constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
+  static_assert(DEPTH >= 2 && DEPTH <= 4, "ring depth");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lg = lane >> 4;
+  const int ln = lane & 15;
+  const uint32_t vz = opaque_zero(p.zero);
+
+  // grid: (split fastest, then block); n_blk indexes column groups
+  const int split = blockIdx.x % p.splits;
+  const int n_blk = KSPLIT ? (int)(blockIdx.x / p.splits) : (int)(blockIdx.x / p.splits) * WPB + wave;
+  const int tn0 = n_blk * NT;
+
+  const uint16_t* a = reinterpret_cast<const uint16_t*>(p.a);
+  const uint16_t* a_row = a + (int64_t)min(ln, p.M - 1) * p.a_stride + 8 * lg;
+
+  const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
+  const uint32_t* bptr = p.b + (int64_t)tn0 * 256 + lane * 4;
+
+  const int total_full = p.K / 128;
+  const int k_tail = p.K - total_full * 128;
+  int s_begin = split * p.steps_per_split;
+  int s_end = min(total_full, s_begin + p.steps_per_split);
+  bool do_tail = (k_tail != 0) && (split == p.splits - 1);
+  if constexpr (KSPLIT) {
+    const int per_wave = (max(s_end - s_begin, 0) + WPB - 1) / WPB;
+    s_begin += wave * per_wave;
+    s_end = min(s_end, s_begin + per_wave);
+    do_tail = do_tail && wave == WPB - 1;
+  }
+
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Integer-operand path (scale after the MFMA) for the integer and fp8 formats with one
+  // scale per column or per >= 128-deep group; dequantize-then-multiply otherwise.
+  using IO = IntOperand<FMT, AT>;
+  constexpr bool INT_B = IO::kEnabled && GSM != GSM_SMALL;
+  constexpr bool ROWSUM = INT_B && IO::kNeedRowSum;
+  f32x4_t rsum = f32x4_t{0.f, 0.f, 0.f, 0.f};  // channelwise: row sums over all of K
+
+  Meta meta_ch[NT];
+  if constexpr (GSM == GSM_CHANNEL && !INT_B) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, 0, 0, (tn0 + t) * 16 + ln));
+  }
+
+  u32x4_t ra[DEPTH][4];       // activations: 4 k32 blocks per step
+  u32x4_t rb[DEPTH][NT][NL];  // weights
+  MetaRaw rm[DEPTH][NT][RAWB];
+
+  auto load_meta = [&](int k0, MetaRaw (&mv)[NT][RAWB]) {
+    if constexpr (GSM == GSM_BIG) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        mv[t][0] = load_meta_raw<FMT, AT>(p, 0, k0 >> p.group_shift, (tn0 + t) * 16 + ln);
+    } else if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          mv[t][b] = load_meta_raw<FMT, AT>(p, 0, (k0 + 32 * b + 8 * lg) >> p.group_shift,
+                                            (tn0 + t) * 16 + ln);
+    }
+  };
+
+  // Issue step s into ring slot dc.
+  auto load = [&](int s, auto dc) {
+    constexpr int d = decltype(dc)::value;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint32_t* tp = bptr + t * 256 + (int64_t)s * NL * chunk_stride;
+#pragma unroll
+      for (int c = 0; c < NL; ++c)
+        rb[d][t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(tp + c * chunk_stride));
+    }
+    const int k0 = s * 128;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) ra[d][b] = *reinterpret_cast<const u32x4_t*>(a_row + k0 + 32 * b);
+    load_meta(k0, rm[d]);
+  };
+
+  auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) {
+    if constexpr (BITS == 4) {
+      w0 = bv[t][0][b];
+      w1 = 0;
+    } else {
+      w0 = bv[t][b >> 1][(b & 1) * 2];
+      w1 = bv[t][b >> 1][(b & 1) * 2 + 1];
+    }
+  };
+
+  auto compute_regs = [&](const u32x4_t (&av)[4], const u32x4_t (&bv)[NT][NL],
+                          const MetaRaw (&mv)[NT][RAWB], int nblocks) {
+    if constexpr (INT_B) {
+      // channelwise: accumulate D and R over all of K; grouped: per step, then scale
+      f32x4_t d[NT];
+      f32x4_t r;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) d[t] = GSM == GSM_CHANNEL ? acc[t] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      r = GSM == GSM_CHANNEL ? rsum : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const u32x4_t ones = u32x4_t{IO::kOnes, IO::kOnes, IO::kOnes, IO::kOnes};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          const u32x4_t ap = BITS == 4 ? a_perm_u4(av[b]) : av[b];
+          if constexpr (ROWSUM) r = mfma16(av[b], ones, r, AT{});
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            uint32_t w0, w1;
+            b_words(bv, t, b, w0, w1);
+            d[t] = mfma16(ap, int_operand<FMT, AT>(w0, w1, vz), d[t], AT{});
+          }
+        }
+      }
+      if constexpr (GSM == GSM_CHANNEL) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = d[t];
+        rsum = r;
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const IMeta m = make_imeta<FMT, AT>(mv[t][0]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = __builtin_fmaf(m.S, d[t][i], acc[t][i]);
+            if constexpr (ROWSUM) v = __builtin_fmaf(-m.C, r[i], v);
+            acc[t][i] = v;
+          }
+        }
+      }
+    } else {
+      Meta mm[NT];
+      if constexpr (GSM == GSM_CHANNEL) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) mm[t] = meta_ch[t];
+      } else if constexpr (GSM == GSM_BIG) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(mv[t][0]);
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(mv[t][b]);
+          }
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            uint32_t w0, w1;
+            b_words(bv, t, b, w0, w1);
+            acc[t] = mfma16(av[b], dequant_operand<FMT, AT>(w0, w1, mm[t], vz), acc[t], AT{});
+          }
+        }
+      }
+    }
+  };
+
+  // Consume ring slot dc.
+  auto compute = [&](auto dc) {
+    constexpr int d = decltype(dc)::value;
+    compute_regs(ra[d], rb[d], rm[d], 4);
+  };
+
+  // ---- main loop ---------------------------------------------------------------------------
+  // Step j lives in slot j % DEPTH; prefetches past the last step are clamped to it (an L2
+  // hit into a slot that is never consumed); the last nsteps % DEPTH steps run after the loop.
+  const int nsteps = max(s_end - s_begin, 0);
+  if (nsteps > 0) {
+    const int last = s_end - 1;
+    static_for<DEPTH - 1>([&](auto dc) { load(min(s_begin + (int)dc, last), dc); });
+    const int full_trips = nsteps / DEPTH;
+    int s = s_begin;
+    for (int i = 0; i < full_trips; ++i, s += DEPTH) {
+      static_for<DEPTH>([&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        load(min(s + d + DEPTH - 1, last), std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{});
+        compute(dc);
+      });
+    }
+    const int rem = nsteps - full_trips * DEPTH;
+    static_for<DEPTH - 1>([&](auto dc) {
+      if ((int)dc < rem) compute(dc);
+    });
+  }
+
+  // ---- K tail ------------------------------------------------------------------------------
+  if (do_tail) {
+    const int nblocks = k_tail / 32;
+    const int kt0 = total_full * 128;
+    u32x4_t av[4];
+    u32x4_t bv[NT][NL];
+    MetaRaw mv[NT][RAWB];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      av[b] = b < nblocks ? *reinterpret_cast<const u32x4_t*>(a_row + kt0 + 32 * b)
+                          : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t n = (int64_t)(tn0 + t) * 16 + ln;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          const int64_t k = kt0 + 32 * b + 8 * lg;
+          if constexpr (BITS == 4) {
+            bv[t][0][b] = p.b[layout_word_index(4, p.K, p.N, n, k)];
+          } else {
+            bv[t][b >> 1][(b & 1) * 2] = p.b[layout_word_index(8, p.K, p.N, n, k)];
+            bv[t][b >> 1][(b & 1) * 2 + 1] = p.b[layout_word_index(8, p.K, p.N, n, k + 4)];
+          }
+        }
+      }
+      if constexpr (GSM == GSM_BIG) {
+        mv[t][0] = load_meta_raw<FMT, AT>(p, 0, kt0 >> p.group_shift, (int)n);
+      } else if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          mv[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, 0, (kt0 + 32 * b + 8 * lg) >> p.group_shift,
+                                                         (int)n)
+                                 : MetaRaw{0u, 0u};
+      }
+    }
+    compute_regs(av, bv, mv, nblocks);
+  }
+
+  // channelwise integer-operand path: apply the column scale / zero point once
+  if constexpr (INT_B && GSM == GSM_CHANNEL) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, 0, 0, (tn0 + t) * 16 + ln));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = m.S * acc[t][i];
+        if constexpr (ROWSUM) v = __builtin_fmaf(-m.C, rsum[i], v);
+        acc[t][i] = v;
+      }
+    }
+  }
+
+  // ---- KSPLIT: add the waves' partial sums --------------------------------------------------
+  if constexpr (KSPLIT && WPB > 1) {
+    __shared__ f32x4_t red[WPB - 1][NT][64];
+    if (wave > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < WPB - 1; ++w)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] += red[w][t][lane];
+  }
+
+  // ---- epilogue ----------------------------------------------------------------------------
+  float alpha = 1.0f;
+  if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[0], p.alpha_exp);
+  const uint16_t* bias = reinterpret_cast<const uint16_t*>(p.bias);
+  uint16_t* cout = reinterpret_cast<uint16_t*>(p.c);
+  auto finish = [&](int row, int col, float v) {
+    float o = v * alpha;
+    if (bias != nullptr)
+      o += raw16_to_float(load_u16<AT>(bias, bias_storage_index(col)), AT{});
+    cout[(int64_t)row * p.N + col] = to_raw16(o, AT{});
+  };
+
+  if (p.splits == 1) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = lg * 4 + e;
+        if (row < p.M) finish(row, (tn0 + t) * 16 + ln, acc[t][e]);
+      }
+    return;
+  }
+
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = lg * 4 + e;
+      if (row < p.M)
+        __hip_atomic_fetch_add(p.ws + (int64_t)row * p.N + (tn0 + t) * 16 + ln, acc[t][e],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  // Same ordering argument as the tiled kernel: completed memory-side atomics, then the
+  // arrival counter; the last arriver reads the sums back with atomic exchanges.
+  wait_vm_all();
+  int prev = 0;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(p.counters + n_blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0);
+  if (prev != p.splits - 1) return;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = lg * 4 + e;
+      if (row < p.M) {
+        const int col = (tn0 + t) * 16 + ln;
+        const float v = __hip_atomic_exchange(p.ws + (int64_t)row * p.N + col, 0.0f,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        finish(row, col, v);
+      }
+    }
+  if (lane == 0)
+    __hip_atomic_store(p.counters + n_blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace mmi

@@ -193,12 +193,29 @@ __device__ __forceinline__ Meta make_meta(MetaRaw raw) {
   return m;
 }
 
-// (x & mask) | bits in one VALU op.  VOP3 on gfx9 takes no literal operands, so the compiler
-// would otherwise emit v_and_b32 + v_or_b32; the constants live in registers instead.
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "s"(bits));
+// (x & MASK) | bits in one v_and_or_b32.  A VOP3 instruction on gfx9 reads no literal and
+// at most one SGPR, so the mask has to sit in a VGPR the optimizer cannot fold back into a
+// literal (which would split the op into v_and + v_or): MASK | vz, where vz is a VGPR
+// holding zero that the compiler cannot prove is zero (opaque_zero()).  The instruction is
+// compiler-generated on purpose: results that feed MFMA operands need the wait states the
+// hazard recognizer inserts after a VALU write, which it never does for inline assembly.
+template <uint32_t MASK>
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t bits, uint32_t vz) {
+  return (x & (MASK | vz)) | bits;
+}
+// Same, for a result consumed half by half (v_fma_mix_f32 op_sel): an empty asm with a
+// read-write VGPR operand emits nothing but hides the value from the optimizer, which would
+// otherwise narrow the op per half and split it back into v_and + v_or.  Only for values
+// that do not feed an MFMA directly.
+template <uint32_t MASK>
+__device__ __forceinline__ uint32_t and_or_halves(uint32_t x, uint32_t bits, uint32_t vz) {
+  uint32_t r = and_or<MASK>(x, bits, vz);
+  asm("" : "+v"(r));
   return r;
+}
+// Zero in a VGPR, from a kernel argument that is always zero.
+__device__ __forceinline__ uint32_t opaque_zero(int zero_arg) {
+  return threadIdx.x & (uint32_t)zero_arg;
 }
 
 __device__ __forceinline__ float h_lo(uint32_t x) {
@@ -211,14 +228,15 @@ __device__ __forceinline__ float h_hi(uint32_t x) {
 // Dequantize the MFMA B operand of one lane: 8 consecutive k of one column.
 // 4-bit formats read w0 only, 8-bit formats read w0 (k0..3) and w1 (k4..7).
 template <int FMT, class AT>
-__device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, const Meta& m) {
+__device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, const Meta& m,
+                                                 uint32_t vz) {
   u32x4_t r;
   if constexpr (FMT == FMT_U4B8 || FMT == FMT_U4) {
-    const uint32_t x0 = and_or(w0, 0x000f000fu, 0x64006400u);  // k0, k4  : 1024 + q
-    const uint32_t x1 = and_or(w0, 0x00f000f0u, 0x64006400u);  // k1, k5  : 1024 + 16q
+    const uint32_t x0 = and_or_halves<0x000f000fu>(w0, 0x64006400u, vz);  // k0, k4  : 1024 + q
+    const uint32_t x1 = and_or_halves<0x00f000f0u>(w0, 0x64006400u, vz);  // k1, k5  : 1024 + 16q
     const uint32_t t = w0 >> 8;
-    const uint32_t x2 = and_or(t, 0x000f000fu, 0x64006400u);  // k2, k6
-    const uint32_t x3 = and_or(t, 0x00f000f0u, 0x64006400u);  // k3, k7
+    const uint32_t x2 = and_or_halves<0x000f000fu>(t, 0x64006400u, vz);  // k2, k6
+    const uint32_t x3 = and_or_halves<0x00f000f0u>(t, 0x64006400u, vz);  // k3, k7
     const float e0 = __builtin_fmaf(h_lo(x0), m.s, m.c1);
     const float e4 = __builtin_fmaf(h_hi(x0), m.s, m.c1);
     const float e1 = __builtin_fmaf(h_lo(x1), m.s16, m.c16);
@@ -232,10 +250,10 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
     r[2] = pack2(e4, e5, AT{});
     r[3] = pack2(e6, e7, AT{});
   } else if constexpr (FMT == FMT_U8B128 || FMT == FMT_U8) {
-    const uint32_t a0 = and_or(w0, 0x00ff00ffu, 0x64006400u);       // k0, k2
-    const uint32_t a1 = and_or(w0 >> 8, 0x00ff00ffu, 0x64006400u);  // k1, k3
-    const uint32_t b0 = and_or(w1, 0x00ff00ffu, 0x64006400u);       // k4, k6
-    const uint32_t b1 = and_or(w1 >> 8, 0x00ff00ffu, 0x64006400u);  // k5, k7
+    const uint32_t a0 = and_or_halves<0x00ff00ffu>(w0, 0x64006400u, vz);       // k0, k2
+    const uint32_t a1 = and_or_halves<0x00ff00ffu>(w0 >> 8, 0x64006400u, vz);  // k1, k3
+    const uint32_t b0 = and_or_halves<0x00ff00ffu>(w1, 0x64006400u, vz);       // k4, k6
+    const uint32_t b1 = and_or_halves<0x00ff00ffu>(w1 >> 8, 0x64006400u, vz);  // k5, k7
     r[0] = pack2(__builtin_fmaf(h_lo(a0), m.s, m.c1), __builtin_fmaf(h_lo(a1), m.s, m.c1),
                  AT{});
     r[1] = pack2(__builtin_fmaf(h_hi(a0), m.s, m.c1), __builtin_fmaf(h_hi(a1), m.s, m.c1),
@@ -301,6 +319,103 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
       r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 2));
       r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, m.s, 3));
     }
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------
+// Integer-operand path: scale after the MFMA.
+//
+// For the integer and fp8 formats the MFMA B operand can carry the code itself instead of
+// the dequantized weight, and the column's scale / zero point is applied once to the fp32
+// partial sum of a whole group:
+//     sum_k a_k w_k = S * D - C * R,   D = sum_k a_k B_k,   R = sum_k a_k (row sum),
+//   u4     B = MAGIC + q       (one v_and_or_b32 per pair: fp16 1024 + q, bf16 128 + q)
+//   u8     B = 1024 + q (fp16, v_perm_b32 with the exponent byte) or q (bf16, exact)
+//   fp8    B = the e4m3 value (hardware conversion, exact in fp16 and bf16)
+// with (S, C) = (s, s*(MAGIC + bias)) for biased codes, (s, s*MAGIC + z) for float zero
+// points and (s/256, 0) for fp8.  Every product a_k*B_k is exact in fp32, so the result
+// differs from dequantize-then-multiply only by the per-weight rounding the latter applies;
+// the dequantize op itself keeps the bit-exact dequant_operand() above.
+// ---------------------------------------------------------------------------------------
+template <int FMT, class AT>
+struct IntOperand {
+  static constexpr bool kEnabled = FMT == FMT_U4B8 || FMT == FMT_U4 || FMT == FMT_U8B128 ||
+                                   FMT == FMT_U8 || FMT == FMT_FP8;
+  static constexpr bool kNeedRowSum = FMT != FMT_FP8;
+  // code offset carried by B: the magic number of the 16-bit pattern
+  static constexpr float kMagic =
+      (fmt_bits(FMT) == 4 || AT::kId == 0) ? (AT::kId == 0 ? 1024.0f : 128.0f) : 0.0f;
+  static constexpr uint32_t kMagicBits = AT::kId == 0 ? 0x64006400u : 0x43004300u;
+  // 1.0 in both halves: B operand of the row-sum MFMA
+  static constexpr uint32_t kOnes = AT::kId == 0 ? 0x3c003c00u : 0x3f803f80u;
+};
+
+struct IMeta {
+  float S;  // multiplies D
+  float C;  // multiplies the row sum R
+};
+
+template <int FMT, class AT>
+__device__ __forceinline__ IMeta make_imeta(MetaRaw raw) {
+  using IO = IntOperand<FMT, AT>;
+  const float s = raw16_to_float(raw.s & 0xffff, AT{});
+  if constexpr (FMT == FMT_FP8) {
+    return IMeta{s * 0.00390625f, 0.0f};
+  } else if constexpr (FMT == FMT_U4B8) {
+    return IMeta{s, s * (IO::kMagic + 8.0f)};
+  } else if constexpr (FMT == FMT_U8B128) {
+    return IMeta{s, s * (IO::kMagic + 128.0f)};
+  } else {
+    const float z = raw16_to_float(raw.z & 0xffff, AT{});
+    return IMeta{s, __builtin_fmaf(s, IO::kMagic, z)};
+  }
+}
+
+// The 4-bit integer operand holds its 8 values in k order [0,4,1,5,2,6,3,7] (one
+// v_and_or_b32 per pair, no repacking of the nibbles); the A operand is permuted to match.
+__device__ __forceinline__ u32x4_t a_perm_u4(const u32x4_t& n) {
+  u32x4_t r;
+  r[0] = __builtin_amdgcn_perm(n[2], n[0], 0x05040100u);  // a0, a4
+  r[1] = __builtin_amdgcn_perm(n[2], n[0], 0x07060302u);  // a1, a5
+  r[2] = __builtin_amdgcn_perm(n[3], n[1], 0x05040100u);  // a2, a6
+  r[3] = __builtin_amdgcn_perm(n[3], n[1], 0x07060302u);  // a3, a7
+  return r;
+}
+
+template <int FMT, class AT>
+__device__ __forceinline__ u32x4_t int_operand(uint32_t w0, uint32_t w1, uint32_t vz) {
+  using IO = IntOperand<FMT, AT>;
+  u32x4_t r;
+  if constexpr (fmt_bits(FMT) == 4) {
+    r[0] = and_or<0x000f000fu>(w0, IO::kMagicBits, vz);
+    r[1] = and_or<0x000f000fu>(w0 >> 4, IO::kMagicBits, vz);
+    r[2] = and_or<0x000f000fu>(w0 >> 8, IO::kMagicBits, vz);
+    r[3] = and_or<0x000f000fu>(w0 >> 12, IO::kMagicBits, vz);
+  } else if constexpr (FMT == FMT_FP8) {
+    if constexpr (AT::kId == 0) {
+      r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false));
+      r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true));
+      r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false));
+      r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true));
+    } else {
+      r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false));
+      r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true));
+      r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false));
+      r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true));
+    }
+  } else if constexpr (AT::kId == 0) {
+    // u8, fp16: bytes [q_i, 0x64] are the fp16 value 1024 + q_i
+    r[0] = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+  } else {
+    // u8, bf16: q < 256 is exact in bf16
+    r[0] = pack2((float)(w0 & 0xffu), (float)((w0 >> 8) & 0xffu), AT{});
+    r[1] = pack2((float)((w0 >> 16) & 0xffu), (float)(w0 >> 24), AT{});
+    r[2] = pack2((float)(w1 & 0xffu), (float)((w1 >> 8) & 0xffu), AT{});
+    r[3] = pack2((float)((w1 >> 16) & 0xffu), (float)(w1 >> 24), AT{});
   }
   return r;
 }

@@ -5,15 +5,36 @@
 
 namespace mmi {
 
+// Launches the kernel, or, when l.occupancy is set, only reports how many of its workgroups
+// fit on one CU.
+template <typename Kernel>
+static hipError_t launch_or_query(const GemmLaunch& l, Kernel kernel, unsigned threads,
+                                  const GemmParams& p, hipStream_t s) {
+  if (l.occupancy != nullptr)
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(l.occupancy, kernel, threads, 0);
+  hipLaunchKernelGGL(kernel, dim3(l.grid), dim3(threads), 0, s, p);
+  return hipGetLastError();
+}
+
 template <int FMT, class AT, int GSM>
 static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
-  const dim3 grid(l.grid), block(256);
-#define MMI_CASE(BM_, NT_, CH_, MOE_)                                                          \
-  if (l.bm == BM_ && l.nt == NT_ && l.ch == CH_ && l.moe == MOE_) {                            \
-    hipLaunchKernelGGL((marlin_gemm_kernel<FMT, AT, BM_, NT_, CH_, GSM, MOE_>), grid, block, 0, \
-                       s, p);                                                                  \
-    return hipGetLastError();                                                                  \
+  if (l.depth > 0) {
+#define MMI_DECODE(NT_, D_, WPB_, KS_)                                                       \
+  if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_)                         \
+    return launch_or_query(l, marlin_decode_kernel<FMT, AT, NT_, D_, WPB_, KS_, GSM>, 64 * WPB_, \
+                           p, s);
+    MMI_DECODE(4, 3, 4, true)
+    MMI_DECODE(4, 3, 2, true)
+    MMI_DECODE(4, 4, 2, true)
+    MMI_DECODE(4, 3, 1, false)
+    MMI_DECODE(4, 4, 1, false)
+    MMI_DECODE(2, 4, 4, true)
+#undef MMI_DECODE
+    return hipErrorInvalidValue;
   }
+#define MMI_CASE(BM_, NT_, CH_, MOE_)                                                     \
+  if (l.bm == BM_ && l.nt == NT_ && l.ch == CH_ && l.moe == MOE_)                         \
+    return launch_or_query(l, marlin_gemm_kernel<FMT, AT, BM_, NT_, CH_, GSM, MOE_>, 256, p, s);
   // dense: small-M weight streaming tiles, then MFMA tiles
   MMI_CASE(16, 1, 1, false)
   MMI_CASE(16, 1, 2, false)

@@ -58,6 +58,7 @@ struct GemmParams {
   int moe_bs;
   int mul_topk;
   int valid_ids;  // size_m * top_k
+  int zero;       // always 0: source of an opaque VGPR zero (opaque_zero())
 };
 
 // Group-size modes.
@@ -160,6 +161,7 @@ void marlin_gemm_kernel(const GemmParams p) {
   const int lane = tid & 63;
   const int lg = lane >> 4;  // lane group: k-slice 8*lg inside a 32-deep block
   const int ln = lane & 15;  // column (B) / row (A) inside a 16-wide fragment
+  const uint32_t vz = opaque_zero(p.zero);
 
   int split, n_blk, m_blk;
   decode_block(p, split, n_blk, m_blk);
@@ -299,7 +301,7 @@ void marlin_gemm_kernel(const GemmParams p) {
             w0 = bw[t][b >> 1][(b & 1) * 2];
             w1 = bw[t][b >> 1][(b & 1) * 2 + 1];
           }
-          const u32x4_t bop = dequant_operand<FMT, AT>(w0, w1, mm[t]);
+          const u32x4_t bop = dequant_operand<FMT, AT>(w0, w1, mm[t], vz);
 #pragma unroll
           for (int i = 0; i < MT; ++i) acc[i][t] = mfma16(af[i], bop, acc[i][t], AT{});
         }

@@ -6,7 +6,7 @@
 
 #include <string>
 
-#include "gemm_kernel.h"
+#include "decode_kernel.h"
 
 namespace mmi {
 
@@ -31,8 +31,12 @@ struct GemmLaunch {
   int bm;    // rows per workgroup
   int nt;    // n16 tiles per wave
   int ch;    // 1 KiB weight chunks per tile per K step
+  int depth;  // > 0: decode kernel with this load ring depth (bm, ch unused)
+  int wpb;    // decode kernel: waves per workgroup
+  bool ksplit;  // decode kernel: the workgroup's waves split K (else: adjacent column groups)
   bool moe;
   unsigned grid;
+  int* occupancy;  // when set: report workgroups per CU instead of launching
 };
 // Defined per format in gemm_<fmt>.hip; returns hipErrorInvalidValue for a configuration
 // that is not instantiated.
