@@ -71,8 +71,9 @@ hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, in
 // moe_align_block_size (reference moe_align_sum_kernels.cu:81-181, 291-320), one workgroup
 // of 1024 threads.  Unlike the reference's atomic scatter, placement is deterministic:
 // route indices of one expert appear in ascending order.  Rounds of 1024 indices are placed
-// in index order; inside a round each wavefront ranks its lanes per expert with ballots and
-// wavefronts are ordered by a per-expert prefix over per-wave counts kept in LDS.
+// in index order; inside a round each wavefront ranks its lanes per expert with one ballot
+// per expert-id bit and wavefronts are ordered by a per-expert prefix over per-wave counts
+// kept in LDS.
 // ---------------------------------------------------------------------------------------
 template <typename IdT>
 __global__ __launch_bounds__(1024) void moe_align_kernel(
@@ -88,6 +89,7 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int ebits = E > 1 ? 32 - __clz(E - 1) : 1;  // bits of the largest expert id
 
   auto mapped = [&](int64_t i) -> int {
     int64_t e = (int64_t)topk[i];
@@ -141,16 +143,17 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(
     const int64_t i = base + tid;
     const int e = i < numel ? mapped(i) : -1;
     for (int x = lane; x < E; x += 64) wave_cnt[wave * E + x] = 0;
-    uint64_t active = __ballot(e >= 0);
-    int rank = 0;
-    while (active) {
-      const int leader = __ffsll((long long)active) - 1;
-      const int le = __shfl(e, leader);
-      const uint64_t same = __ballot(e == le) & active;
-      if (e == le) rank = __popcll(same & ((1ull << lane) - 1));
-      if (lane == leader) wave_cnt[wave * E + le] = (uint8_t)__popcll(same);
-      active &= ~same;
+    // lanes holding the same expert: intersect, over the id's bits, the ballots that agree
+    // with this lane's bit (no per-expert loop)
+    uint64_t same = __ballot(e >= 0);
+    for (int bit = 0; bit < ebits; ++bit) {
+      const int set = (e >> bit) & 1;
+      const uint64_t m = __ballot(set);
+      same &= set ? m : ~m;
     }
+    const uint64_t before = same & ((1ull << lane) - 1);
+    const int rank = __popcll(before);
+    if (e >= 0 && before == 0) wave_cnt[wave * E + e] = (uint8_t)__popcll(same);
     __syncthreads();
     if (e >= 0) {
       int pos = cursor[e] + rank;

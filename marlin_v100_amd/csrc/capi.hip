@@ -158,7 +158,8 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
 
 // ---- tile selection -------------------------------------------------------------------
 struct Plan {
-  int bm, nt, ch, depth, wpb, ksplit, splits, steps_per_split, n_blocks, m_blocks, xcd_group_m;
+  int bm, nt, ch, depth, wpb, ksplit, stream, splits, steps_per_split, n_blocks, m_blocks,
+      xcd_group_m;
   int64_t grid;
 };
 
@@ -167,9 +168,9 @@ hipError_t dispatch_gemm(const GemmLaunch& l, const GemmParams& p, hipStream_t s
 // Workgroups of one kernel instance that fit on a CU at once (cached per instance).
 int blocks_per_cu(const GemmLaunch& l) {
   static std::mutex mu;
-  static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int>, int> cache;
+  static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int, int>, int> cache;
   const auto key = std::make_tuple(l.fmt, (int)l.bf16, l.gsm, l.bm, l.nt, l.ch, l.depth, l.wpb,
-                                   (int)l.ksplit, (int)l.moe);
+                                   (int)l.ksplit, (int)l.stream, (int)l.moe);
   std::lock_guard<std::mutex> lock(mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
@@ -240,6 +241,40 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
       p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
       p.grid = blocks_n * p.splits;
+      return p;
+    }
+  }
+  // 16..64-row blocks: the multistage kernel (all of K's operands three steps ahead).
+  if (M <= 128 && env_int("MARLIN_MI355X_STREAM", 1) != 0) {
+    const int bm = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
+    int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
+    if (bm > 16 && nt == 1) nt = 0;  // not instantiated: fall through to the tiled kernel
+    nt = env_int("MARLIN_MI355X_STREAM_NT", nt);
+    const bool small_meta_fits = !(kinds.gsm == GSM_SMALL && bm >= 48);
+    if (nt > 0 && N % (64 * nt) == 0 && small_meta_fits) {
+      p.bm = bm;
+      p.nt = nt;
+      p.ch = 1;
+      p.stream = 1;
+      p.m_blocks = (int)((M + bm - 1) / bm);
+      p.n_blocks = (int)(N / (64 * nt));
+      p.xcd_group_m = 0;
+      GemmLaunch q = kinds;
+      q.bm = bm;
+      q.nt = nt;
+      q.ch = 1;
+      q.stream = true;
+      const int64_t resident = (int64_t)blocks_per_cu(q) * cus;
+      const int64_t base = (int64_t)p.m_blocks * p.n_blocks;
+      const int steps = (int)(K / 128);
+      int splits = 1;
+      if (base < resident && steps >= 8)
+        splits = (int)std::min<int64_t>(resident / base, steps / 4);
+      splits = env_int("MARLIN_MI355X_SPLIT_K", splits);
+      splits = std::max(1, std::min(splits, std::max(steps, 1)));
+      p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
+      p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
+      p.grid = base * p.splits;
       return p;
     }
   }
@@ -546,6 +581,7 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     l.depth = plan.depth;
     l.wpb = plan.wpb;
     l.ksplit = plan.ksplit != 0;
+    l.stream = plan.stream != 0;
     l.moe = false;
     l.grid = (unsigned)plan.grid;
     check_hip(dispatch_gemm(l, p, s), "marlin_gemm launch");
@@ -715,7 +751,27 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     l.nt = nt;
     l.ch = 1;
     l.moe = true;
+    l.stream = !(mc.gsm == GSM_SMALL && bm >= 48) && env_int("MARLIN_MI355X_STREAM", 1) != 0;
     l.grid = (unsigned)((int64_t)m_blocks * n_blocks * splits);
+    // Few routes per expert (decode-sized batches): the K-split decode kernel on 16-row parts
+    // of each moe block, one part and 64 columns per workgroup; parts without routes exit at
+    // once.  Its integer-operand path needs integer or fp8 weights with >= 128-deep groups.
+    const bool int_operand = mc.fmt != FMT_MXFP4 && mc.fmt != FMT_NVFP4 && mc.gsm != GSM_SMALL;
+    if (int_operand && size_m * top_k <= 16 * num_experts &&
+        env_int("MARLIN_MI355X_MOE_DECODE", 1) != 0) {
+      const int parts = (int)((moe_block_size + 15) / 16);
+      const int groups = (int)(size_n / 64);
+      p.splits = 1;
+      p.steps_per_split = steps;
+      p.num_n_blocks = groups;
+      p.num_m_blocks = m_blocks;
+      l.stream = false;
+      l.depth = 3;
+      l.nt = 4;
+      l.wpb = env_int("MARLIN_MI355X_MOE_WPB", steps >= 24 ? 4 : 2);  // >= 6 steps per wave
+      l.ksplit = true;
+      l.grid = (unsigned)((int64_t)m_blocks * parts * groups);
+    }
     check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");
   });
 }

@@ -40,8 +40,9 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM>
+template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM, bool MOE>
 __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParams p) {
+  static_assert(!MOE || KSPLIT, "MoE blocks use the K-split workgroup layout");
   constexpr int BITS = fmt_bits(FMT);
   constexpr int NL = (BITS == 4) ? 1 : 2;  // 1 KiB chunks per tile per 128-deep step
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
@@ -53,16 +54,43 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   const int ln = lane & 15;
   const uint32_t vz = opaque_zero(p.zero);
 
-  // grid: (split fastest, then block); n_blk indexes column groups
+  // grid: (split fastest, then block); n_blk indexes column groups.  MoE (reference
+  // sm70_marlin_gemm.cuh:3591-3686): blocks are (16-row part of a moe block, column group),
+  // column group fastest; rows are gathered by route id / top_k and scattered to route id.
   const int split = blockIdx.x % p.splits;
-  const int n_blk = KSPLIT ? (int)(blockIdx.x / p.splits) : (int)(blockIdx.x / p.splits) * WPB + wave;
+  const int blk = blockIdx.x / p.splits;
+  int n_blk = KSPLIT ? blk : blk * WPB + wave;
+  int expert = 0;
+  int row_id = -1;  // MoE: route index of the activation row this lane supplies
+  if constexpr (MOE) {
+    // parts slowest: the first (always live) part of every block is scheduled before the
+    // later parts, which small batches leave empty
+    n_blk = blk % p.num_n_blocks;
+    const int m_blk = (blk / p.num_n_blocks) % p.num_m_blocks;
+    const int part = (blk / p.num_n_blocks) / p.num_m_blocks;
+    const int padded = p.num_post_pad[0];
+    if (m_blk * p.moe_bs >= padded || m_blk >= p.expert_ids_numel) return;
+    expert = p.expert_ids[m_blk];
+    if (expert < 0) return;
+    const int r = part * 16 + ln;
+    const int si = m_blk * p.moe_bs + r;
+    if (r < p.moe_bs && si < p.sorted_numel && si < padded) {
+      const int id = p.sorted_ids[si];
+      if (id >= 0 && id < p.valid_ids) row_id = id;
+    }
+    // every wave of the workgroup sees the same rows: a part without routes exits whole
+    if (__ballot(row_id >= 0) == 0) return;
+  }
   const int tn0 = n_blk * NT;
 
   const uint16_t* a = reinterpret_cast<const uint16_t*>(p.a);
-  const uint16_t* a_row = a + (int64_t)min(ln, p.M - 1) * p.a_stride + 8 * lg;
+  const int64_t a_r = MOE ? (row_id >= 0 ? row_id / p.top_k : 0) : min(ln, p.M - 1);
+  const uint16_t* a_row = a + a_r * p.a_stride + 8 * lg;
 
   const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
-  const uint32_t* bptr = p.b + (int64_t)tn0 * 256 + lane * 4;
+  const uint32_t* bbase = p.b + (int64_t)expert * p.b_expert_stride;
+  const uint32_t* bptr = bbase + (int64_t)tn0 * 256 + lane * 4;
+  const int64_t meta_base = (int64_t)expert * p.meta_expert_stride;
 
   const int total_full = p.K / 128;
   const int k_tail = p.K - total_full * 128;
@@ -91,30 +119,30 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   if constexpr (GSM == GSM_CHANNEL && !INT_B) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, 0, 0, (tn0 + t) * 16 + ln));
+      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
   }
 
   u32x4_t ra[DEPTH][4];       // activations: 4 k32 blocks per step
   u32x4_t rb[DEPTH][NT][NL];  // weights
   MetaRaw rm[DEPTH][NT][RAWB];
 
-  auto load_meta = [&](int k0, MetaRaw (&mv)[NT][RAWB]) {
+  auto load_meta = [&](int k0, MetaRaw (&mv)[NT][RAWB]) __attribute__((always_inline)) {
     if constexpr (GSM == GSM_BIG) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        mv[t][0] = load_meta_raw<FMT, AT>(p, 0, k0 >> p.group_shift, (tn0 + t) * 16 + ln);
+        mv[t][0] = load_meta_raw<FMT, AT>(p, meta_base, k0 >> p.group_shift, (tn0 + t) * 16 + ln);
     } else if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          mv[t][b] = load_meta_raw<FMT, AT>(p, 0, (k0 + 32 * b + 8 * lg) >> p.group_shift,
+          mv[t][b] = load_meta_raw<FMT, AT>(p, meta_base, (k0 + 32 * b + 8 * lg) >> p.group_shift,
                                             (tn0 + t) * 16 + ln);
     }
   };
 
   // Issue step s into ring slot dc.
-  auto load = [&](int s, auto dc) {
+  auto load = [&](int s, auto dc) __attribute__((always_inline)) {
     constexpr int d = decltype(dc)::value;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -129,7 +157,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
     load_meta(k0, rm[d]);
   };
 
-  auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) {
+  auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) __attribute__((always_inline)) {
     if constexpr (BITS == 4) {
       w0 = bv[t][0][b];
       w1 = 0;
@@ -140,7 +168,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   };
 
   auto compute_regs = [&](const u32x4_t (&av)[4], const u32x4_t (&bv)[NT][NL],
-                          const MetaRaw (&mv)[NT][RAWB], int nblocks) {
+                          const MetaRaw (&mv)[NT][RAWB], int nblocks) __attribute__((always_inline)) {
     if constexpr (INT_B) {
       // channelwise: accumulate D and R over all of K; grouped: per step, then scale
       f32x4_t d[NT];
@@ -206,7 +234,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   };
 
   // Consume ring slot dc.
-  auto compute = [&](auto dc) {
+  auto compute = [&](auto dc) __attribute__((always_inline)) {
     constexpr int d = decltype(dc)::value;
     compute_regs(ra[d], rb[d], rm[d], 4);
   };
@@ -252,19 +280,19 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
         if (b < nblocks) {
           const int64_t k = kt0 + 32 * b + 8 * lg;
           if constexpr (BITS == 4) {
-            bv[t][0][b] = p.b[layout_word_index(4, p.K, p.N, n, k)];
+            bv[t][0][b] = bbase[layout_word_index(4, p.K, p.N, n, k)];
           } else {
-            bv[t][b >> 1][(b & 1) * 2] = p.b[layout_word_index(8, p.K, p.N, n, k)];
-            bv[t][b >> 1][(b & 1) * 2 + 1] = p.b[layout_word_index(8, p.K, p.N, n, k + 4)];
+            bv[t][b >> 1][(b & 1) * 2] = bbase[layout_word_index(8, p.K, p.N, n, k)];
+            bv[t][b >> 1][(b & 1) * 2 + 1] = bbase[layout_word_index(8, p.K, p.N, n, k + 4)];
           }
         }
       }
       if constexpr (GSM == GSM_BIG) {
-        mv[t][0] = load_meta_raw<FMT, AT>(p, 0, kt0 >> p.group_shift, (int)n);
+        mv[t][0] = load_meta_raw<FMT, AT>(p, meta_base, kt0 >> p.group_shift, (int)n);
       } else if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          mv[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, 0, (kt0 + 32 * b + 8 * lg) >> p.group_shift,
+          mv[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, meta_base, (kt0 + 32 * b + 8 * lg) >> p.group_shift,
                                                          (int)n)
                                  : MetaRaw{0u, 0u};
       }
@@ -276,7 +304,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   if constexpr (INT_B && GSM == GSM_CHANNEL) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, 0, 0, (tn0 + t) * 16 + ln));
+      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = m.S * acc[t][i];
@@ -303,15 +331,37 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
 
   // ---- epilogue ----------------------------------------------------------------------------
   float alpha = 1.0f;
-  if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[0], p.alpha_exp);
+  if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[expert], p.alpha_exp);
   const uint16_t* bias = reinterpret_cast<const uint16_t*>(p.bias);
   uint16_t* cout = reinterpret_cast<uint16_t*>(p.c);
-  auto finish = [&](int row, int col, float v) {
+  auto finish = [&](int row, int col, float v) __attribute__((always_inline)) {
     float o = v * alpha;
-    if (bias != nullptr)
-      o += raw16_to_float(load_u16<AT>(bias, bias_storage_index(col)), AT{});
+    if (bias != nullptr) {
+      float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
+                                AT{});
+      if constexpr (MOE) {
+        if (p.mul_topk) bv *= alpha;
+      }
+      o += bv;
+    }
+    if constexpr (MOE) {
+      if (p.mul_topk) o *= p.topk_w[row];
+    }
     cout[(int64_t)row * p.N + col] = to_raw16(o, AT{});
   };
+
+  if constexpr (MOE) {
+    // accumulator row lg*4+e belongs to the route held by lane lg*4+e (splits == 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int id = __shfl(row_id, lg * 4 + e);
+      if (id >= 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) finish(id, (tn0 + t) * 16 + ln, acc[t][e]);
+      }
+    }
+    return;
+  }
 
   if (p.splits == 1) {
 #pragma unroll

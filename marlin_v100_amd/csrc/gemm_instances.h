@@ -19,17 +19,40 @@ static hipError_t launch_or_query(const GemmLaunch& l, Kernel kernel, unsigned t
 template <int FMT, class AT, int GSM>
 static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
   if (l.depth > 0) {
-#define MMI_DECODE(NT_, D_, WPB_, KS_)                                                       \
-  if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_)                         \
-    return launch_or_query(l, marlin_decode_kernel<FMT, AT, NT_, D_, WPB_, KS_, GSM>, 64 * WPB_, \
-                           p, s);
-    MMI_DECODE(4, 3, 4, true)
-    MMI_DECODE(4, 3, 2, true)
-    MMI_DECODE(4, 4, 2, true)
-    MMI_DECODE(4, 3, 1, false)
-    MMI_DECODE(4, 4, 1, false)
-    MMI_DECODE(2, 4, 4, true)
+#define MMI_DECODE(NT_, D_, WPB_, KS_, MOE_)                                                 \
+  if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_ && l.moe == MOE_)        \
+    return launch_or_query(l, marlin_decode_kernel<FMT, AT, NT_, D_, WPB_, KS_, GSM, MOE_>,     \
+                           64 * WPB_, p, s);
+    MMI_DECODE(4, 3, 4, true, false)
+    MMI_DECODE(4, 3, 2, true, false)
+    MMI_DECODE(4, 4, 2, true, false)
+    MMI_DECODE(4, 3, 1, false, false)
+    MMI_DECODE(2, 4, 4, true, false)
+    MMI_DECODE(4, 3, 4, true, true)
+    MMI_DECODE(4, 3, 2, true, true)
 #undef MMI_DECODE
+    return hipErrorInvalidValue;
+  }
+  if (l.stream) {
+// (per-32/64 group metadata for 48/64-row blocks does not fit the register budget: those
+// stay on marlin_gemm_kernel)
+#define MMI_STREAM(BM_, NT_, MOE_)                                                          \
+  if constexpr (!(GSM == GSM_SMALL && BM_ >= 48)) {                                         \
+    if (l.bm == BM_ && l.nt == NT_ && l.moe == MOE_)                                        \
+      return launch_or_query(l, marlin_stream_kernel<FMT, AT, BM_, NT_, GSM, MOE_>, 256, p, s); \
+  }
+    MMI_STREAM(16, 1, false)
+    MMI_STREAM(16, 2, false)
+    MMI_STREAM(16, 4, false)
+    MMI_STREAM(32, 2, false)
+    MMI_STREAM(32, 4, false)
+    MMI_STREAM(64, 2, false)
+    MMI_STREAM(64, 4, false)
+    MMI_STREAM(16, 4, true)
+    MMI_STREAM(32, 4, true)
+    MMI_STREAM(48, 4, true)
+    MMI_STREAM(64, 4, true)
+#undef MMI_STREAM
     return hipErrorInvalidValue;
   }
 #define MMI_CASE(BM_, NT_, CH_, MOE_)                                                     \

@@ -6,7 +6,7 @@
 
 #include <string>
 
-#include "decode_kernel.h"
+#include "stream_kernel.h"
 
 namespace mmi {
 
@@ -34,6 +34,7 @@ struct GemmLaunch {
   int depth;  // > 0: decode kernel with this load ring depth (bm, ch unused)
   int wpb;    // decode kernel: waves per workgroup
   bool ksplit;  // decode kernel: the workgroup's waves split K (else: adjacent column groups)
+  bool stream;  // multistage kernel for 16..64-row blocks (bm, nt, moe; ch unused)
   bool moe;
   unsigned grid;
   int* occupancy;  // when set: report workgroups per CU instead of launching

@@ -1,0 +1,447 @@
+// stream_kernel.h -- multistage mixed-precision GEMM for 16..64-row blocks, gfx950.
+//
+// One workgroup = 4 wavefronts computes a BM x BN block (BN = 4 waves x NT n16 tiles); the
+// waves share the BM activation rows and own disjoint columns.  Every operand of a K step
+// (128 deep) is fetched three steps before it is multiplied, and nothing waits for more
+// than the data it is about to use:
+//   * weights (one dwordx4 of the chunk-major layout, device_common.h, per lane, tile and
+//     1 KiB chunk), scale metadata and each wave's quarter of the activation tile are
+//     loaded into a ring of three register sets;
+//   * one step before use, each wave writes its quarter of the activation tile from the
+//     ring into one of three LDS buffers (fragment-major, so every A-operand ds_read_b128 is
+//     conflict-free); one barrier per step publishes it.  (Activations are not copied with
+//     global_load_lds_dwordx4: the compiler's wait-count insertion cannot tell the buffers of
+//     such a ring apart and would wait for every pending load before each LDS read.);
+//   * slots and buffers are compile-time indices (static_for), the loop body is
+//     branch-free, and prefetches past the last step are clamped to it, so the compiler's
+//     vmcnt bookkeeping is exact on every trip;
+//   * with at most two m-tiles, integer and fp8 weights with channelwise or >= 128-deep
+//     groups use the integer-operand path (device_common.h): codes feed the MFMA, the scale / zero point is applied per
+//     group to the fp32 partial sums; the 4-bit activation permutation it needs is applied
+//     once, by the wave that stages the fragment;
+//   * split-K, the XCD-aware block order, the MoE row gather / scatter and the epilogue are
+//     those of marlin_gemm_kernel (gemm_kernel.h).
+#pragma once
+
+#include "decode_kernel.h"
+
+namespace mmi {
+
+template <int FMT, class AT, int BM, int NT, int GSM, bool MOE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void marlin_stream_kernel(const GemmParams p) {
+  constexpr int MT = BM / 16;
+  constexpr int BITS = fmt_bits(FMT);
+  constexpr int BN = 4 * NT * 16;
+  constexpr int NL = (BITS == 4) ? 1 : 2;  // 1 KiB chunk loads per tile per step
+  constexpr int FRAGS = 4 * MT;             // A fragments per step (4 k32 blocks x MT)
+  constexpr int FPW = MT;                   // A fragments staged by each wave
+  constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
+  constexpr int D = 3;  // ring depth (register sets and LDS buffers)
+  using IO = IntOperand<FMT, AT>;
+  // (the per-group scaling keeps a second set of MT x NT accumulators: at most two m-tiles)
+  constexpr bool INT_B = IO::kEnabled && GSM != GSM_SMALL && MT <= 2;
+  constexpr bool ROWSUM = INT_B && IO::kNeedRowSum;
+
+  __shared__ u32x4_t lds_a0[FRAGS * 64];
+  __shared__ u32x4_t lds_a1[FRAGS * 64];
+  __shared__ u32x4_t lds_a2[FRAGS * 64];
+  __shared__ int lds_rows[BM];
+  __shared__ int lds_last;
+  using Buf = u32x4_t[FRAGS * 64];
+  auto buf = [&](auto dc) __attribute__((always_inline)) -> Buf& {
+    constexpr int d = decltype(dc)::value;
+    if constexpr (d == 0) return lds_a0;
+    else if constexpr (d == 1) return lds_a1;
+    else return lds_a2;
+  };
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lg = lane >> 4;
+  const int ln = lane & 15;
+  const uint32_t vz = opaque_zero(p.zero);
+
+  int split, n_blk, m_blk;
+  decode_block(p, split, n_blk, m_blk);
+  const int out_tile = m_blk * p.num_n_blocks + n_blk;
+
+  int expert = 0;
+  const uint16_t* a = reinterpret_cast<const uint16_t*>(p.a);
+  if constexpr (MOE) {
+    const int padded = p.num_post_pad[0];
+    if (m_blk * p.moe_bs >= padded || m_blk >= p.expert_ids_numel) return;
+    expert = p.expert_ids[m_blk];
+    if (expert < 0) return;
+    for (int r = tid; r < BM; r += 256) {
+      int id = -1;
+      const int si = m_blk * p.moe_bs + r;
+      if (r < p.moe_bs && si < p.sorted_numel && si < padded) {
+        id = p.sorted_ids[si];
+        if (id < 0 || id >= p.valid_ids) id = -1;
+      }
+      lds_rows[r] = id;
+    }
+    __syncthreads();
+  }
+  const int m0 = MOE ? 0 : m_blk * BM;
+
+  // Fragments staged by this wave: f = wave + 4*i covers k32 block f / MT, m16 tile f % MT.
+  const uint16_t* a_src[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wave + 4 * i;
+    const int b = f / MT;
+    const int r = (f % MT) * 16 + ln;
+    int64_t row;
+    if constexpr (MOE) {
+      const int id = lds_rows[r];
+      row = id >= 0 ? id / p.top_k : 0;
+    } else {
+      row = min(m0 + r, p.M - 1);
+    }
+    a_src[i] = a + row * p.a_stride + 32 * b + 8 * lg;
+  }
+
+  const int tn0 = n_blk * (BN / 16) + wave * NT;
+  const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
+  const uint32_t* bptr = p.b + (int64_t)expert * p.b_expert_stride + (int64_t)tn0 * 256 + lane * 4;
+  const int64_t meta_base = (int64_t)expert * p.meta_expert_stride;
+
+  const int total_full = p.K / 128;
+  const int k_tail = p.K - total_full * 128;
+  const int s_begin = split * p.steps_per_split;
+  const int s_end = min(total_full, s_begin + p.steps_per_split);
+  const bool do_tail = (k_tail != 0) && (split == p.splits - 1);
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x4_t rsum[MT];  // channelwise integer-operand path: row sums over all of K
+#pragma unroll
+  for (int i = 0; i < MT; ++i) rsum[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  Meta meta_ch[NT];
+  if constexpr (GSM == GSM_CHANNEL && !INT_B) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
+  }
+
+  u32x4_t ra[D][FPW];
+  u32x4_t rb[D][NT][NL];
+  MetaRaw rm[D][NT][RAWB];
+
+  auto load = [&](int s, auto dc) __attribute__((always_inline)) {
+    constexpr int d = decltype(dc)::value;
+    const int k0 = s * 128;
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) ra[d][i] = *reinterpret_cast<const u32x4_t*>(a_src[i] + k0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint32_t* tp = bptr + t * 256 + (int64_t)s * NL * chunk_stride;
+#pragma unroll
+      for (int c = 0; c < NL; ++c)
+        rb[d][t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(tp + c * chunk_stride));
+    }
+    if constexpr (GSM == GSM_BIG) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        rm[d][t][0] = load_meta_raw<FMT, AT>(p, meta_base, k0 >> p.group_shift, (tn0 + t) * 16 + ln);
+    } else if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          rm[d][t][b] = load_meta_raw<FMT, AT>(p, meta_base, (k0 + 32 * b + 8 * lg) >> p.group_shift,
+                                               (tn0 + t) * 16 + ln);
+    }
+  };
+
+  // Write this wave's fragments of ring slot dc into LDS buffer dc.
+  auto stage = [&](auto dc) __attribute__((always_inline)) {
+    constexpr int d = decltype(dc)::value;
+    Buf& lb = buf(dc);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) {
+      const int f = wave + 4 * i;
+      lb[f * 64 + lane] = (INT_B && BITS == 4) ? a_perm_u4(ra[d][i]) : ra[d][i];
+    }
+  };
+
+  auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) __attribute__((always_inline)) {
+    if constexpr (BITS == 4) {
+      w0 = bv[t][0][b];
+      w1 = 0;
+    } else {
+      w0 = bv[t][b >> 1][(b & 1) * 2];
+      w1 = bv[t][b >> 1][(b & 1) * 2 + 1];
+    }
+  };
+
+  // Multiply one step: activations from LDS buffer lb, weights / metadata from registers.
+  auto compute_core = [&](const Buf& lb, const u32x4_t (&bv)[NT][NL],
+                          const MetaRaw (&mv)[NT][RAWB], int nblocks) __attribute__((always_inline)) {
+    if constexpr (INT_B) {
+      f32x4_t d[MT][NT];
+      f32x4_t r[MT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        r[i] = GSM == GSM_CHANNEL ? rsum[i] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          d[i][t] = GSM == GSM_CHANNEL ? acc[i][t] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      const u32x4_t ones = u32x4_t{IO::kOnes, IO::kOnes, IO::kOnes, IO::kOnes};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          u32x4_t af[MT];
+#pragma unroll
+          for (int i = 0; i < MT; ++i) af[i] = lb[(b * MT + i) * 64 + lane];
+          if constexpr (ROWSUM) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i) r[i] = mfma16(af[i], ones, r[i], AT{});
+          }
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            uint32_t w0, w1;
+            b_words(bv, t, b, w0, w1);
+            const u32x4_t bop = int_operand<FMT, AT>(w0, w1, vz);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) d[i][t] = mfma16(af[i], bop, d[i][t], AT{});
+          }
+        }
+      }
+      if constexpr (GSM == GSM_CHANNEL) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          rsum[i] = r[i];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[i][t] = d[i][t];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const IMeta m = make_imeta<FMT, AT>(mv[t][0]);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float v = __builtin_fmaf(m.S, d[i][t][e], acc[i][t][e]);
+              if constexpr (ROWSUM) v = __builtin_fmaf(-m.C, r[i][e], v);
+              acc[i][t][e] = v;
+            }
+        }
+      }
+    } else {
+      Meta mm[NT];
+      if constexpr (GSM == GSM_CHANNEL) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) mm[t] = meta_ch[t];
+      } else if constexpr (GSM == GSM_BIG) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(mv[t][0]);
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) mm[t] = make_meta<FMT, AT>(mv[t][b]);
+          }
+          u32x4_t af[MT];
+#pragma unroll
+          for (int i = 0; i < MT; ++i) af[i] = lb[(b * MT + i) * 64 + lane];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            uint32_t w0, w1;
+            b_words(bv, t, b, w0, w1);
+            const u32x4_t bop = dequant_operand<FMT, AT>(w0, w1, mm[t], vz);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) acc[i][t] = mfma16(af[i], bop, acc[i][t], AT{});
+          }
+        }
+      }
+    }
+  };
+
+  // ---- main loop ---------------------------------------------------------------------------
+  // Step j: registers in slot j % 3, activations in LDS buffer j % 3.  Trip j issues the
+  // loads of step j+2, stages the activations of step j+1, multiplies step j, then one
+  // barrier: buffer (j+1) % 3 is published and nobody still reads the buffer the next trip
+  // overwrites.
+  const int nsteps = max(s_end - s_begin, 0);
+  if (nsteps > 0) {
+    const int last = s_end - 1;
+    load(s_begin, std::integral_constant<int, 0>{});
+    load(min(s_begin + 1, last), std::integral_constant<int, 1>{});
+    stage(std::integral_constant<int, 0>{});
+    __syncthreads();
+    const int full_trips = nsteps / D;
+    int s = s_begin;
+    auto trip = [&](auto dc) __attribute__((always_inline)) {
+      constexpr int d = decltype(dc)::value;
+      load(min(s + d + 2, last), std::integral_constant<int, (d + 2) % D>{});
+      stage(std::integral_constant<int, (d + 1) % D>{});
+      compute_core(buf(dc), rb[d], rm[d], 4);
+      __syncthreads();
+    };
+    for (int i = 0; i < full_trips; ++i, s += D) static_for<D>(trip);
+    const int rem = nsteps - full_trips * D;
+    // remaining steps: s, s+1 (slots 0, 1); their loads and staging were issued above
+    if (rem > 0) {
+      stage(std::integral_constant<int, 1>{});
+      compute_core(lds_a0, rb[0], rm[0], 4);
+      __syncthreads();
+      if (rem > 1) compute_core(lds_a1, rb[1], rm[1], 4);
+    }
+  }
+
+  // ---- K tail: (K % 128) / 32 blocks, read word by word through the layout map -----------
+  if (do_tail) {
+    const int nblocks = k_tail / 32;
+    const int kt0 = total_full * 128;
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) {
+      const int f = wave + 4 * i;
+      const int b = f / MT;
+      u32x4_t v = b < nblocks ? *reinterpret_cast<const u32x4_t*>(a_src[i] + kt0)
+                              : u32x4_t{0u, 0u, 0u, 0u};
+      lds_a2[f * 64 + lane] = (INT_B && BITS == 4) ? a_perm_u4(v) : v;
+    }
+    u32x4_t bw[NT][NL];
+    MetaRaw raw[NT][RAWB];
+    const uint32_t* base = p.b + (int64_t)expert * p.b_expert_stride;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t n = (int64_t)(tn0 + t) * 16 + ln;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          const int64_t k = kt0 + 32 * b + 8 * lg;
+          if constexpr (BITS == 4) {
+            bw[t][0][b] = base[layout_word_index(4, p.K, p.N, n, k)];
+          } else {
+            bw[t][b >> 1][(b & 1) * 2] = base[layout_word_index(8, p.K, p.N, n, k)];
+            bw[t][b >> 1][(b & 1) * 2 + 1] = base[layout_word_index(8, p.K, p.N, n, k + 4)];
+          }
+        }
+      }
+      if constexpr (GSM == GSM_BIG) {
+        raw[t][0] = load_meta_raw<FMT, AT>(p, meta_base, kt0 >> p.group_shift, (int)n);
+      } else if constexpr (GSM == GSM_SMALL) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          raw[t][b] = b < nblocks ? load_meta_raw<FMT, AT>(p, meta_base,
+                                                          (kt0 + 32 * b + 8 * lg) >> p.group_shift,
+                                                          (int)n)
+                                  : MetaRaw{0u, 0u};
+      }
+    }
+    __syncthreads();
+    compute_core(lds_a2, bw, raw, nblocks);
+  }
+
+  if constexpr (INT_B && GSM == GSM_CHANNEL) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = m.S * acc[i][t][e];
+          if constexpr (ROWSUM) v = __builtin_fmaf(-m.C, rsum[i][e], v);
+          acc[i][t][e] = v;
+        }
+    }
+  }
+
+  // ---- epilogue --------------------------------------------------------------------------
+  float alpha = 1.0f;
+  if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[expert], p.alpha_exp);
+  const uint16_t* bias = reinterpret_cast<const uint16_t*>(p.bias);
+  uint16_t* cout = reinterpret_cast<uint16_t*>(p.c);
+
+  auto out_row = [&](int r) __attribute__((always_inline)) -> int64_t {  // -1: not stored
+    if constexpr (MOE) {
+      return lds_rows[r];
+    } else {
+      return (m0 + r < p.M) ? (int64_t)(m0 + r) : -1;
+    }
+  };
+
+  auto finish = [&](int r, int col, float v) __attribute__((always_inline)) {
+    const int64_t orow = out_row(r);
+    if (orow < 0) return;
+    float o = v * alpha;
+    if (bias != nullptr) {
+      float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
+                                AT{});
+      if constexpr (MOE) {
+        if (p.mul_topk) bv *= alpha;
+      }
+      o += bv;
+    }
+    if constexpr (MOE) {
+      if (p.mul_topk) o *= p.topk_w[orow];
+    }
+    cout[orow * p.N + col] = to_raw16(o, AT{});
+  };
+
+  if (p.splits == 1) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          finish(i * 16 + lg * 4 + e, (tn0 + t) * 16 + ln, acc[i][t][e]);
+    return;
+  }
+
+  // split-K (same protocol as marlin_gemm_kernel)
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t orow = out_row(i * 16 + lg * 4 + e);
+        if (orow >= 0)
+          __hip_atomic_fetch_add(p.ws + orow * p.N + (tn0 + t) * 16 + ln, acc[i][t][e],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+  wait_vm_all();
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(p.counters + out_tile, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    lds_last = (prev == p.splits - 1);
+  }
+  __syncthreads();
+  if (!lds_last) return;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = i * 16 + lg * 4 + e;
+        const int64_t orow = out_row(r);
+        if (orow >= 0) {
+          const int col = (tn0 + t) * 16 + ln;
+          const float v = __hip_atomic_exchange(p.ws + orow * p.N + col, 0.0f, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+          finish(r, col, v);
+        }
+      }
+  if (tid == 0)
+    __hip_atomic_store(p.counters + out_tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace mmi
