@@ -753,24 +753,25 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     l.moe = true;
     l.stream = !(mc.gsm == GSM_SMALL && bm >= 48) && env_int("MARLIN_MI355X_STREAM", 1) != 0;
     l.grid = (unsigned)((int64_t)m_blocks * n_blocks * splits);
-    // Few routes per expert (decode-sized batches): the K-split decode kernel on 16-row parts
-    // of each moe block, one part and 64 columns per workgroup; parts without routes exit at
-    // once.  Its integer-operand path needs integer or fp8 weights with >= 128-deep groups.
+    // Few routes per expert (decode-sized batches): the K-split decode kernel, one moe block
+    // and 64 columns per workgroup, multiplying only the block's 16-row parts that hold
+    // routes.  Its integer-operand path needs integer or fp8 weights with >= 128-deep groups.
     const bool int_operand = mc.fmt != FMT_MXFP4 && mc.fmt != FMT_NVFP4 && mc.gsm != GSM_SMALL;
     if (int_operand && size_m * top_k <= 16 * num_experts &&
         env_int("MARLIN_MI355X_MOE_DECODE", 1) != 0) {
-      const int parts = (int)((moe_block_size + 15) / 16);
       const int groups = (int)(size_n / 64);
       p.splits = 1;
       p.steps_per_split = steps;
       p.num_n_blocks = groups;
       p.num_m_blocks = m_blocks;
       l.stream = false;
-      l.depth = 3;
+      l.depth = env_int("MARLIN_MI355X_MOE_DEPTH", 3);
       l.nt = 4;
-      l.wpb = env_int("MARLIN_MI355X_MOE_WPB", steps >= 24 ? 4 : 2);  // >= 6 steps per wave
+      // one wave per workgroup, all of K: thousands of short workgroups that the dispatcher
+      // load-balances across CUs as they finish
+      l.wpb = env_int("MARLIN_MI355X_MOE_WPB", 1);
       l.ksplit = true;
-      l.grid = (unsigned)((int64_t)m_blocks * parts * groups);
+      l.grid = (unsigned)((int64_t)m_blocks * groups);
     }
     check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");
   });

@@ -55,33 +55,38 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   const uint32_t vz = opaque_zero(p.zero);
 
   // grid: (split fastest, then block); n_blk indexes column groups.  MoE (reference
-  // sm70_marlin_gemm.cuh:3591-3686): blocks are (16-row part of a moe block, column group),
-  // column group fastest; rows are gathered by route id / top_k and scattered to route id.
+  // sm70_marlin_gemm.cuh:3591-3686): blocks are (moe block, column group), column group
+  // fastest; the moe block's rows (<= 64) are read with one load per lane, and only its
+  // 16-row parts that hold routes are multiplied, one after the other.  Rows are gathered by
+  // route id / top_k and scattered to route id.
   const int split = blockIdx.x % p.splits;
   const int blk = blockIdx.x / p.splits;
   int n_blk = KSPLIT ? blk : blk * WPB + wave;
   int expert = 0;
-  int row_id = -1;  // MoE: route index of the activation row this lane supplies
+  int route = -1;      // MoE: route index of block row `lane`
+  uint64_t live = 1;   // MoE: rows holding routes
+  int nparts = 1;
   if constexpr (MOE) {
-    // parts slowest: the first (always live) part of every block is scheduled before the
-    // later parts, which small batches leave empty
     n_blk = blk % p.num_n_blocks;
-    const int m_blk = (blk / p.num_n_blocks) % p.num_m_blocks;
-    const int part = (blk / p.num_n_blocks) / p.num_m_blocks;
+    const int m_blk = blk / p.num_n_blocks;
     const int padded = p.num_post_pad[0];
     if (m_blk * p.moe_bs >= padded || m_blk >= p.expert_ids_numel) return;
     expert = p.expert_ids[m_blk];
     if (expert < 0) return;
-    const int r = part * 16 + ln;
-    const int si = m_blk * p.moe_bs + r;
-    if (r < p.moe_bs && si < p.sorted_numel && si < padded) {
+    const int si = m_blk * p.moe_bs + lane;
+    if (lane < p.moe_bs && si < p.sorted_numel && si < padded) {
       const int id = p.sorted_ids[si];
-      if (id >= 0 && id < p.valid_ids) row_id = id;
+      if (id >= 0 && id < p.valid_ids) route = id;
     }
-    // every wave of the workgroup sees the same rows: a part without routes exits whole
-    if (__ballot(row_id >= 0) == 0) return;
+    live = __ballot(route >= 0);
+    nparts = (p.moe_bs + 15) >> 4;
   }
   const int tn0 = n_blk * NT;
+
+  for (int part = 0; part < nparts; ++part) {
+  // (every wave of the workgroup sees the same rows, so the part loop is uniform)
+  if (MOE && ((live >> (16 * part)) & 0xffffull) == 0) continue;
+  const int row_id = MOE ? __shfl(route, part * 16 + ln) : -1;
 
   const uint16_t* a = reinterpret_cast<const uint16_t*>(p.a);
   const int64_t a_r = MOE ? (row_id >= 0 ? row_id / p.top_k : 0) : min(ln, p.M - 1);
@@ -322,11 +327,18 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
       for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
     }
     __syncthreads();
-    if (wave > 0) return;
+    if (wave == 0) {
 #pragma unroll
-    for (int w = 0; w < WPB - 1; ++w)
+      for (int w = 0; w < WPB - 1; ++w)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] += red[w][t][lane];
+        for (int t = 0; t < NT; ++t) acc[t] += red[w][t][lane];
+    }
+    if constexpr (MOE) {
+      __syncthreads();  // the next part reuses red
+      if (wave > 0) continue;
+    } else {
+      if (wave > 0) return;
+    }
   }
 
   // ---- epilogue ----------------------------------------------------------------------------
@@ -360,7 +372,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
         for (int t = 0; t < NT; ++t) finish(id, (tn0 + t) * 16 + ln, acc[t][e]);
       }
     }
-    return;
+    continue;
   }
 
   if (p.splits == 1) {
@@ -405,6 +417,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
     }
   if (lane == 0)
     __hip_atomic_store(p.counters + n_blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }  // part loop
 }
 
 }  // namespace mmi

@@ -28,8 +28,13 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     MMI_DECODE(4, 4, 2, true, false)
     MMI_DECODE(4, 3, 1, false, false)
     MMI_DECODE(2, 4, 4, true, false)
+    MMI_DECODE(4, 4, 4, true, false)
     MMI_DECODE(4, 3, 4, true, true)
     MMI_DECODE(4, 3, 2, true, true)
+    MMI_DECODE(4, 4, 4, true, true)
+    MMI_DECODE(4, 4, 2, true, true)
+    MMI_DECODE(4, 3, 1, true, true)
+    MMI_DECODE(4, 4, 1, true, true)
 #undef MMI_DECODE
     return hipErrorInvalidValue;
   }
