@@ -364,7 +364,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": head["alg_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["alg_GBs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": "mmi::marlin_gemm_kernel<FMT_U4, BF16, 16, *, GSM_BIG, false>",
+                     "kernel": "mmi::marlin_decode_kernel<FMT_U4, BF16, NT=4, DEPTH=3, "
+                               "WPB=4, KSPLIT, GSM_BIG, dense>",
                      "algorithmic_bytes_per_launch": head["alg_bytes"]},
         "configs": configs,
     }
