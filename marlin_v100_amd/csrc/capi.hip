@@ -158,30 +158,38 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
 
 // ---- tile selection -------------------------------------------------------------------
 struct Plan {
-  int bm, nt, ch, depth, wpb, ksplit, stream, splits, steps_per_split, n_blocks, m_blocks,
-      xcd_group_m;
+  int bm, nt, ch, depth, wpb, ksplit, occ, stream, splits, steps_per_split, main_blocks, n_blocks,
+      m_blocks, xcd_group_m;
   int64_t grid;
 };
 
 hipError_t dispatch_gemm(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
 
-// Workgroups of one kernel instance that fit on a CU at once (cached per instance).
-int blocks_per_cu(const GemmLaunch& l) {
+// Workgroups of one kernel instance that fit on a CU at once, and whether its registers
+// spill to scratch (cached per instance).
+struct Fit {
+  int blocks_per_cu;
+  bool spills;
+};
+Fit kernel_fit(const GemmLaunch& l) {
   static std::mutex mu;
-  static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int, int>, int> cache;
+  static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int, int, int>, Fit> cache;
   const auto key = std::make_tuple(l.fmt, (int)l.bf16, l.gsm, l.bm, l.nt, l.ch, l.depth, l.wpb,
-                                   (int)l.ksplit, (int)l.stream, (int)l.moe);
+                                   (int)l.ksplit, l.occ, (int)l.stream, (int)l.moe);
   std::lock_guard<std::mutex> lock(mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   GemmLaunch q = l;
-  int occ = 0;
+  int occ = 0, scratch = 0;
   q.occupancy = &occ;
+  q.scratch = &scratch;
   GemmParams dummy{};
-  if (dispatch_gemm(q, dummy, nullptr) != hipSuccess || occ < 1) occ = 1;
-  cache.emplace(key, occ);
-  return occ;
+  Fit f{1, false};
+  if (dispatch_gemm(q, dummy, nullptr) == hipSuccess) f = Fit{std::max(occ, 1), scratch > 0};
+  cache.emplace(key, f);
+  return f;
 }
+int blocks_per_cu(const GemmLaunch& l) { return kernel_fit(l).blocks_per_cu; }
 
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
@@ -190,15 +198,16 @@ int env_int(const char* name, int dflt) {
 
 // Dense selector.
 //  * M <= 16 (decode) is weight-bandwidth bound: the decode kernel, each wave NT n16 tiles,
-//    loads DEPTH-1 K steps ahead, WPB waves per workgroup on adjacent columns.  All of its
-//    workgroups must be resident at once -- a second, partial round of workgroups would
-//    stream its weights alone at the end -- so K is split across workgroups only as far as
-//    the grid still fits on the chip in one round.
+//    DEPTH-1 K steps in flight, the WPB waves of a workgroup splitting K.  The grid must be
+//    resident in one round -- a second, partial round would stream its weights alone at the
+//    end -- and spread evenly over the CUs: each CU takes the same number of whole column
+//    groups and the groups left over are split along K into about one small block per CU.
+//    With fewer groups than CUs, K is split across blocks within an atomics budget.
 //  * 16 < M <= 32 is still weight bound: 32-row blocks with split-K until the grid holds
 //    about 4 workgroups per CU.
 //  * Larger M is MFMA bound: 64x256 or 128x256 blocks (each wave 64/128 x 64) visited in the
 //    XCD-aware grouped order; split-K only when the grid cannot cover the CUs once.
-// MARLIN_MI355X_DECODE="nt,depth,wpb" (nt 0 disables the decode kernel),
+// MARLIN_MI355X_DECODE="nt,depth,wpb,ksplit,occ" (nt 0 disables the decode kernel),
 // MARLIN_MI355X_TILE="bm,nt,ch" and MARLIN_MI355X_SPLIT_K override the choice (tuning).
 Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& kinds) {
   Plan p{};
@@ -207,9 +216,16 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
   // dequantize per weight and stay on the tiled kernel.
   const bool int_operand = kinds.fmt != FMT_MXFP4 && kinds.fmt != FMT_NVFP4 && kinds.gsm != GSM_SMALL;
   if (M <= 16 && (int_operand || getenv("MARLIN_MI355X_DECODE") != nullptr)) {
-    int nt = 4, depth = 3, wpb = 4, ksplit = 1;
-    if (const char* t = getenv("MARLIN_MI355X_DECODE"))
-      sscanf(t, "%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit);
+    int nt = 4, depth = 3, wpb = 4, ksplit = 1, occ = 3;
+    if (const char* t = getenv("MARLIN_MI355X_DECODE")) {
+      sscanf(t, "%d,%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit, &occ);
+    } else {
+      // three waves per SIMD where the instance's registers fit that budget without
+      // spilling (checked once per instance); the compiler's choice otherwise
+      GemmLaunch q = kinds;
+      q.bm = 16, q.nt = nt, q.ch = 1, q.depth = depth, q.wpb = wpb, q.ksplit = true, q.occ = 3;
+      if (kernel_fit(q).spills) occ = 1;
+    }
     if (nt > 0 && N % (16 * nt) == 0) {
       const int64_t groups = N / (16 * nt);
       while (!ksplit && wpb > 1 && groups % wpb != 0) wpb /= 2;
@@ -219,6 +235,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       p.depth = depth;
       p.wpb = wpb;
       p.ksplit = ksplit;
+      p.occ = occ;
       p.m_blocks = 1;
       p.n_blocks = (int)groups;  // split-K counters are per column group
       p.xcd_group_m = 0;
@@ -229,18 +246,44 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       q.depth = depth;
       q.wpb = wpb;
       q.ksplit = ksplit != 0;
+      q.occ = occ;
       const int64_t resident = (int64_t)blocks_per_cu(q) * cus;
       const int64_t blocks_n = ksplit ? groups : groups / wpb;
       const int steps = (int)(K / 128);
       int splits = 1;
-      const int min_steps = 2 * (ksplit ? wpb : 1);  // per split
-      if (blocks_n < resident && steps >= 2 * min_steps)
-        splits = (int)std::min<int64_t>(resident / blocks_n, steps / min_steps);
-      splits = env_int("MARLIN_MI355X_SPLIT_K", splits);
+      int64_t main_blocks = 0;
+      if (blocks_n >= cus && blocks_n < resident) {
+        // Every CU gets the same number of whole column groups; the groups left over are
+        // split along K into about one small block per CU, so that no CU carries a whole
+        // extra group (an extra group on a few CUs sets the span of the launch).
+        main_blocks = blocks_n - blocks_n % cus;
+        const int64_t left = blocks_n - main_blocks;
+        if (left > 0) {
+          const int min_steps = ksplit ? wpb : 1;
+          splits = (int)std::min<int64_t>(std::min<int64_t>(cus / left, (resident - main_blocks) / left),
+                                          steps / std::max(min_steps, 1));
+          splits = std::max(splits, 1);
+        }
+        if (splits == 1) main_blocks = 0;
+      } else if (blocks_n < resident) {
+        // fewer groups than CUs: split K across blocks, as far as the device-scope atomics
+        // of the partial sums stay cheap (about 256K of them per call)
+        const int min_steps = 2 * (ksplit ? wpb : 1);  // per split
+        if (steps >= 2 * min_steps)
+          splits = (int)std::min<int64_t>(resident / blocks_n, steps / min_steps);
+        const int64_t budget = std::max<int64_t>(1, (int64_t(1) << 18) / std::max<int64_t>(M * N, 1));
+        splits = (int)std::min<int64_t>(splits, budget);
+        splits = std::max(splits, 1);
+      }
+      if (const char* t = getenv("MARLIN_MI355X_SPLIT_K")) {
+        splits = atoi(t);
+        main_blocks = 0;
+      }
       splits = std::max(1, std::min(splits, std::max(steps, 1)));
       p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
       p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
-      p.grid = blocks_n * p.splits;
+      p.main_blocks = (int)main_blocks;
+      p.grid = main_blocks + (blocks_n - main_blocks) * p.splits;
       return p;
     }
   }
@@ -566,6 +609,7 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     p.group_shift = mc.group_shift;
     p.splits = plan.splits;
     p.steps_per_split = plan.steps_per_split;
+    p.main_blocks = plan.main_blocks;
     p.num_n_blocks = plan.n_blocks;
     p.num_m_blocks = plan.m_blocks;
     p.xcd_group_m = plan.xcd_group_m;
@@ -581,6 +625,7 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     l.depth = plan.depth;
     l.wpb = plan.wpb;
     l.ksplit = plan.ksplit != 0;
+    l.occ = plan.occ;
     l.stream = plan.stream != 0;
     l.moe = false;
     l.grid = (unsigned)plan.grid;
@@ -771,6 +816,7 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
       // load-balances across CUs as they finish
       l.wpb = env_int("MARLIN_MI355X_MOE_WPB", 1);
       l.ksplit = true;
+      l.occ = 1;
       l.grid = (unsigned)((int64_t)m_blocks * groups);
     }
     check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");

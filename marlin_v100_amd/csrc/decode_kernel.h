@@ -40,16 +40,23 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM, bool MOE>
-__global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParams p) {
+// OCC: waves per SIMD the register allocation must allow (1 = compiler's choice).  At
+// OCC >= 3 the activation slices, which hit in L2, are loaded one step later than the weights
+// (ALEAD < DEPTH - 1), so fewer ring slots are live at once.
+template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM, bool MOE, int OCC>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(OCC, 8)))
+void marlin_decode_kernel(const GemmParams p) {
   static_assert(!MOE || KSPLIT, "MoE blocks use the K-split workgroup layout");
   constexpr int BITS = fmt_bits(FMT);
   constexpr int NL = (BITS == 4) ? 1 : 2;  // 1 KiB chunks per tile per 128-deep step
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
   static_assert(DEPTH >= 2 && DEPTH <= 4, "ring depth");
+  constexpr int ALEAD = (OCC >= 3 && DEPTH >= 3) ? DEPTH - 2 : DEPTH - 1;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // (readfirstlane: the wave index is uniform, so the K range, the loop counter and the
+  // per-step addresses derived from it live in SGPRs)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lg = lane >> 4;
   const int ln = lane & 15;
   const uint32_t vz = opaque_zero(p.zero);
@@ -59,8 +66,19 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   // fastest; the moe block's rows (<= 64) are read with one load per lane, and only its
   // 16-row parts that hold routes are multiplied, one after the other.  Rows are gathered by
   // route id / top_k and scattered to route id.
-  const int split = blockIdx.x % p.splits;
-  const int blk = blockIdx.x / p.splits;
+  // Blocks [0, nleft) split K `splits` ways over the column groups from main_blocks on; they
+  // come first so that their waves are the oldest on each CU (issue priority goes to older
+  // waves) and their short K ranges and atomics finish under the main blocks' streaming.
+  // Blocks from nleft on take one whole column group each.
+  const int nleft = (int)gridDim.x - p.main_blocks;
+  int split = 0;
+  int blk = (int)blockIdx.x - nleft;
+  int nsplit = 1;
+  if ((int)blockIdx.x < nleft) {
+    split = blockIdx.x % p.splits;
+    blk = p.main_blocks + blockIdx.x / p.splits;
+    nsplit = p.splits;
+  }
   int n_blk = KSPLIT ? blk : blk * WPB + wave;
   int expert = 0;
   int route = -1;      // MoE: route index of block row `lane`
@@ -100,8 +118,8 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   const int total_full = p.K / 128;
   const int k_tail = p.K - total_full * 128;
   int s_begin = split * p.steps_per_split;
-  int s_end = min(total_full, s_begin + p.steps_per_split);
-  bool do_tail = (k_tail != 0) && (split == p.splits - 1);
+  int s_end = nsplit == 1 ? total_full : min(total_full, s_begin + p.steps_per_split);
+  bool do_tail = (k_tail != 0) && (split == nsplit - 1);
   if constexpr (KSPLIT) {
     const int per_wave = (max(s_end - s_begin, 0) + WPB - 1) / WPB;
     s_begin += wave * per_wave;
@@ -146,9 +164,13 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
     }
   };
 
-  // Issue step s into ring slot dc.
-  auto load = [&](int s, auto dc) __attribute__((always_inline)) {
+  // Issue the weights and metadata of step s into ring slot dc.
+  // (issue_order: the prologue and the loop issue weights, metadata and activations in the
+  // same fixed order, so the wait counts the compiler derives for the loop header hold on
+  // both paths into it and keep DEPTH-1 steps in flight.)
+  auto load_b = [&](int s, auto dc) __attribute__((always_inline)) {
     constexpr int d = decltype(dc)::value;
+    issue_order();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const uint32_t* tp = bptr + t * 256 + (int64_t)s * NL * chunk_stride;
@@ -156,10 +178,18 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
       for (int c = 0; c < NL; ++c)
         rb[d][t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(tp + c * chunk_stride));
     }
+    issue_order();
+    load_meta(s * 128, rm[d]);
+    issue_order();
+  };
+  // Issue the activation slices of step s into ring slot dc.
+  auto load_a = [&](int s, auto dc) __attribute__((always_inline)) {
+    constexpr int d = decltype(dc)::value;
     const int k0 = s * 128;
+    issue_order();
 #pragma unroll
     for (int b = 0; b < 4; ++b) ra[d][b] = *reinterpret_cast<const u32x4_t*>(a_row + k0 + 32 * b);
-    load_meta(k0, rm[d]);
+    issue_order();
   };
 
   auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) __attribute__((always_inline)) {
@@ -245,24 +275,33 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   };
 
   // ---- main loop ---------------------------------------------------------------------------
-  // Step j lives in slot j % DEPTH; prefetches past the last step are clamped to it (an L2
-  // hit into a slot that is never consumed); the last nsteps % DEPTH steps run after the loop.
+  // Step j lives in slot j % DEPTH; its weights are issued DEPTH-1 steps ahead, its
+  // activations ALEAD steps ahead.  Each trip issues the activations before the weights so
+  // that waiting for step j's activations never waits for a younger step's weights.
+  // Prefetches past the last step are clamped to it (an L2 hit into a slot that is never
+  // consumed); the last nsteps % DEPTH steps run after the loop.
   const int nsteps = max(s_end - s_begin, 0);
   if (nsteps > 0) {
     const int last = s_end - 1;
-    static_for<DEPTH - 1>([&](auto dc) { load(min(s_begin + (int)dc, last), dc); });
+    static_for<ALEAD>([&](auto dc) { load_a(min(s_begin + (int)dc, last), dc); });
+    static_for<DEPTH - 1>([&](auto dc) { load_b(min(s_begin + (int)dc, last), dc); });
     const int full_trips = nsteps / DEPTH;
     int s = s_begin;
     for (int i = 0; i < full_trips; ++i, s += DEPTH) {
       static_for<DEPTH>([&](auto dc) {
         constexpr int d = decltype(dc)::value;
-        load(min(s + d + DEPTH - 1, last), std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{});
+        load_a(min(s + d + ALEAD, last), std::integral_constant<int, (d + ALEAD) % DEPTH>{});
+        load_b(min(s + d + DEPTH - 1, last), std::integral_constant<int, (d + DEPTH - 1) % DEPTH>{});
         compute(dc);
       });
     }
     const int rem = nsteps - full_trips * DEPTH;
     static_for<DEPTH - 1>([&](auto dc) {
-      if ((int)dc < rem) compute(dc);
+      constexpr int d = decltype(dc)::value;
+      if (d < rem) {
+        if constexpr (d >= ALEAD) load_a(s + d, dc);
+        compute(dc);
+      }
     });
   }
 
@@ -375,7 +414,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
     continue;
   }
 
-  if (p.splits == 1) {
+  if (nsplit == 1) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -402,7 +441,7 @@ __global__ __launch_bounds__(64 * WPB) void marlin_decode_kernel(const GemmParam
   if (lane == 0)
     prev = __hip_atomic_fetch_add(p.counters + n_blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   prev = __shfl(prev, 0);
-  if (prev != p.splits - 1) return;
+  if (prev != nsplit - 1) return;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll

@@ -10,8 +10,15 @@ namespace mmi {
 template <typename Kernel>
 static hipError_t launch_or_query(const GemmLaunch& l, Kernel kernel, unsigned threads,
                                   const GemmParams& p, hipStream_t s) {
-  if (l.occupancy != nullptr)
+  if (l.occupancy != nullptr) {
+    if (l.scratch != nullptr) {
+      hipFuncAttributes attr{};
+      const hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel));
+      if (e != hipSuccess) return e;
+      *l.scratch = (int)attr.localSizeBytes;
+    }
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(l.occupancy, kernel, threads, 0);
+  }
   hipLaunchKernelGGL(kernel, dim3(l.grid), dim3(threads), 0, s, p);
   return hipGetLastError();
 }
@@ -19,22 +26,26 @@ static hipError_t launch_or_query(const GemmLaunch& l, Kernel kernel, unsigned t
 template <int FMT, class AT, int GSM>
 static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
   if (l.depth > 0) {
-#define MMI_DECODE(NT_, D_, WPB_, KS_, MOE_)                                                 \
-  if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_ && l.moe == MOE_)        \
-    return launch_or_query(l, marlin_decode_kernel<FMT, AT, NT_, D_, WPB_, KS_, GSM, MOE_>,     \
+#define MMI_DECODE(NT_, D_, WPB_, KS_, MOE_, OCC_)                                           \
+  if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_ && l.moe == MOE_ &&       \
+      l.occ == OCC_)                                                                         \
+    return launch_or_query(l, marlin_decode_kernel<FMT, AT, NT_, D_, WPB_, KS_, GSM, MOE_, OCC_>, \
                            64 * WPB_, p, s);
-    MMI_DECODE(4, 3, 4, true, false)
-    MMI_DECODE(4, 3, 2, true, false)
-    MMI_DECODE(4, 4, 2, true, false)
-    MMI_DECODE(4, 3, 1, false, false)
-    MMI_DECODE(2, 4, 4, true, false)
-    MMI_DECODE(4, 4, 4, true, false)
-    MMI_DECODE(4, 3, 4, true, true)
-    MMI_DECODE(4, 3, 2, true, true)
-    MMI_DECODE(4, 4, 4, true, true)
-    MMI_DECODE(4, 4, 2, true, true)
-    MMI_DECODE(4, 3, 1, true, true)
-    MMI_DECODE(4, 4, 1, true, true)
+    MMI_DECODE(4, 3, 4, true, false, 1)
+    MMI_DECODE(4, 3, 4, true, false, 3)
+    MMI_DECODE(4, 2, 4, true, false, 3)
+    MMI_DECODE(4, 2, 4, true, false, 4)
+    MMI_DECODE(4, 3, 2, true, false, 1)
+    MMI_DECODE(4, 4, 2, true, false, 1)
+    MMI_DECODE(4, 3, 1, false, false, 1)
+    MMI_DECODE(2, 4, 4, true, false, 1)
+    MMI_DECODE(4, 4, 4, true, false, 1)
+    MMI_DECODE(4, 3, 4, true, true, 1)
+    MMI_DECODE(4, 3, 2, true, true, 1)
+    MMI_DECODE(4, 4, 4, true, true, 1)
+    MMI_DECODE(4, 4, 2, true, true, 1)
+    MMI_DECODE(4, 3, 1, true, true, 1)
+    MMI_DECODE(4, 4, 1, true, true, 1)
 #undef MMI_DECODE
     return hipErrorInvalidValue;
   }

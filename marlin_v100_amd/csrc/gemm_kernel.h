@@ -42,6 +42,8 @@ struct GemmParams {
   int group_shift;  // log2(group size) for grouped modes
   int splits;
   int steps_per_split;
+  int main_blocks;  // decode kernel: the last main_blocks blocks take all of K unsplit; the
+                    // blocks before them split K `splits` ways (0: every block splits)
   int num_n_blocks;
   int num_m_blocks;
   int xcd_group_m;  // m-blocks per group in the XCD-aware order (0: plain order)
@@ -95,6 +97,11 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, void* lds_wave_base)
 }
 
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Keeps the compiler from reordering memory instructions across this point (emits nothing).
+// The vmcnt a consumer waits for is counted from the issue order of the loads, so a ring of
+// loads only keeps its depth if every path into the loop issues them in the same order.
+__device__ __forceinline__ void issue_order() { asm volatile("" ::: "memory"); }
 
 // Workgroup id -> (split, n block, m block).  Dense launches use the XCD-aware grouped
 // order when p.xcd_group_m > 0; MoE launches keep the plain order (one moe block per row).

@@ -34,10 +34,12 @@ struct GemmLaunch {
   int depth;  // > 0: decode kernel with this load ring depth (bm, ch unused)
   int wpb;    // decode kernel: waves per workgroup
   bool ksplit;  // decode kernel: the workgroup's waves split K (else: adjacent column groups)
+  int occ;      // decode kernel: waves per SIMD its registers must allow (1: compiler's choice)
   bool stream;  // multistage kernel for 16..64-row blocks (bm, nt, moe; ch unused)
   bool moe;
   unsigned grid;
   int* occupancy;  // when set: report workgroups per CU instead of launching
+  int* scratch;    // with occupancy: also report the kernel's scratch bytes per lane
 };
 // Defined per format in gemm_<fmt>.hip; returns hipErrorInvalidValue for a configuration
 // that is not instantiated.
