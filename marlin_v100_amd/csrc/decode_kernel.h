@@ -109,6 +109,15 @@ void marlin_decode_kernel(const GemmParams p) {
   const uint16_t* a = reinterpret_cast<const uint16_t*>(p.a);
   const int64_t a_r = MOE ? (row_id >= 0 ? row_id / p.top_k : 0) : min(ln, p.M - 1);
   const uint16_t* a_row = a + a_r * p.a_stride + 8 * lg;
+  // Dense blocks load each step's activations line by line (lane l of load b takes 16
+  // bytes of row 4b + l/16 at k offset 8*(l%16), so a load covers four whole rows) and pass
+  // them through a per-wave LDS tile into the MFMA operand layout, instead of 16 rows x 64
+  // bytes per load: half the L1 cache-line requests for the same bytes.
+  constexpr bool ATX = !MOE;
+  int a_off[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    a_off[b] = min(4 * b + (lane >> 4), p.M - 1) * (int)p.a_stride + 8 * (lane & 15);
 
   const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
   const uint32_t* bbase = p.b + (int64_t)expert * p.b_expert_stride;
@@ -188,7 +197,9 @@ void marlin_decode_kernel(const GemmParams p) {
     const int k0 = s * 128;
     issue_order();
 #pragma unroll
-    for (int b = 0; b < 4; ++b) ra[d][b] = *reinterpret_cast<const u32x4_t*>(a_row + k0 + 32 * b);
+    for (int b = 0; b < 4; ++b)
+      ra[d][b] = ATX ? *reinterpret_cast<const u32x4_t*>(a + a_off[b] + k0)
+                     : *reinterpret_cast<const u32x4_t*>(a_row + k0 + 32 * b);
     issue_order();
   };
 
@@ -203,8 +214,49 @@ void marlin_decode_kernel(const GemmParams p) {
   };
 
   auto compute_regs = [&](const u32x4_t (&av)[4], const u32x4_t (&bv)[NT][NL],
-                          const MetaRaw (&mv)[NT][RAWB], int nblocks) __attribute__((always_inline)) {
-    if constexpr (INT_B) {
+                          const MetaRaw (&mv)[NT][RAWB], int nblocks, auto permuted)
+                          __attribute__((always_inline)) {
+    constexpr bool PERMUTED = decltype(permuted)::value;
+    if constexpr (INT_B && GSM != GSM_CHANNEL && OCC >= 3) {
+      // grouped, register-lean order: the step's row sums first, then the tiles two at a
+      // time, each pair scaled into acc as soon as its four k32 blocks are multiplied
+      f32x4_t r = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const u32x4_t ones = u32x4_t{IO::kOnes, IO::kOnes, IO::kOnes, IO::kOnes};
+      if constexpr (ROWSUM) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (b < nblocks) r = mfma16(av[b], ones, r, AT{});
+      }
+      constexpr int TP = NT >= 2 ? 2 : 1;
+#pragma unroll
+      for (int t0 = 0; t0 < NT; t0 += TP) {
+        f32x4_t d[TP];
+#pragma unroll
+        for (int u = 0; u < TP; ++u) d[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          if (b < nblocks) {
+            const u32x4_t ap = (BITS == 4 && !PERMUTED) ? a_perm_u4(av[b]) : av[b];
+#pragma unroll
+            for (int u = 0; u < TP; ++u) {
+              uint32_t w0, w1;
+              b_words(bv, t0 + u, b, w0, w1);
+              d[u] = mfma16(ap, int_operand<FMT, AT>(w0, w1, vz), d[u], AT{});
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < TP; ++u) {
+          const IMeta m = make_imeta<FMT, AT>(mv[t0 + u][0]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = __builtin_fmaf(m.S, d[u][i], acc[t0 + u][i]);
+            if constexpr (ROWSUM) v = __builtin_fmaf(-m.C, r[i], v);
+            acc[t0 + u][i] = v;
+          }
+        }
+      }
+    } else if constexpr (INT_B) {
       // channelwise: accumulate D and R over all of K; grouped: per step, then scale
       f32x4_t d[NT];
       f32x4_t r;
@@ -215,7 +267,7 @@ void marlin_decode_kernel(const GemmParams p) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         if (b < nblocks) {
-          const u32x4_t ap = BITS == 4 ? a_perm_u4(av[b]) : av[b];
+          const u32x4_t ap = (BITS == 4 && !PERMUTED) ? a_perm_u4(av[b]) : av[b];
           if constexpr (ROWSUM) r = mfma16(av[b], ones, r, AT{});
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
@@ -268,10 +320,28 @@ void marlin_decode_kernel(const GemmParams p) {
     }
   };
 
-  // Consume ring slot dc.
+  // Consume ring slot dc.  (ATX: piece (row r, k chunk c) of the step is MFMA block c/4,
+  // lane (c%4)*16 + r; the row index is XOR-swizzled with c so that neither the 16 lanes
+  // writing one row nor the 64 lanes reading one block collide on LDS banks.  A wave's own
+  // LDS accesses complete in order, so the tile is rewritten each step without a barrier.)
+  __shared__ u32x4_t lds_at[ATX ? WPB : 1][4 * 64];
   auto compute = [&](auto dc) __attribute__((always_inline)) {
     constexpr int d = decltype(dc)::value;
-    compute_regs(ra[d], rb[d], rm[d], 4);
+    if constexpr (ATX) {
+      constexpr bool PERM = BITS == 4 && INT_B;
+      const int c = lane & 15;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int r = 4 * b + (lane >> 4);
+        lds_at[wave][(c >> 2) * 64 + (c & 3) * 16 + (r ^ c)] = PERM ? a_perm_u4(ra[d][b]) : ra[d][b];
+      }
+      u32x4_t av[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) av[b] = lds_at[wave][b * 64 + lg * 16 + (ln ^ (b * 4 + lg))];
+      compute_regs(av, rb[d], rm[d], 4, std::integral_constant<bool, PERM>{});
+    } else {
+      compute_regs(ra[d], rb[d], rm[d], 4, std::false_type{});
+    }
   };
 
   // ---- main loop ---------------------------------------------------------------------------
@@ -341,7 +411,7 @@ void marlin_decode_kernel(const GemmParams p) {
                                  : MetaRaw{0u, 0u};
       }
     }
-    compute_regs(av, bv, mv, nblocks);
+    compute_regs(av, bv, mv, nblocks, std::false_type{});
   }
 
   // channelwise integer-operand path: apply the column scale / zero point once
