@@ -365,7 +365,7 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(head["alg_GBs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "kernel": "mmi::marlin_decode_kernel<FMT_U4, BF16, NT=4, DEPTH=3, "
-                               "WPB=4, KSPLIT, GSM_BIG, dense>",
+                               "WPB=4, KSPLIT, GSM_BIG, dense, OCC=3>",
                      "algorithmic_bytes_per_launch": head["alg_bytes"]},
         "configs": configs,
     }
