@@ -6,23 +6,28 @@
 //   * each wave owns NT n16 tiles (16*NT columns) and a range of K steps (128 deep).  The
 //     WPB waves of a workgroup either split the K range of one column group (KSPLIT: their
 //     partial sums are added through LDS once at the end, no global atomics) or own
-//     adjacent column groups over the same K range (they then read the same activation
-//     slices at about the same time and share them through the CU's L1 cache);
+//     adjacent column groups over the same K range;
 //   * per step each lane loads one dwordx4 of the chunk-major weight layout
-//     (device_common.h) per tile, its activation slice (8 values of row l%16; rows >= M
-//     read row M-1) and the step's scale metadata into a register ring of DEPTH slots, so
-//     DEPTH-1 steps are in flight while one is multiplied.  (A ring in LDS, filled by
-//     global_load_lds_dwordx4, would save the registers, but the compiler's wait-count
-//     insertion does not tell the slots of such a ring apart and waits for every pending
-//     copy before each LDS read, which serializes the pipeline.);
-//   * slots are compile-time indices (static_for), the loop body is branch-free, so the
-//     compiler's vmcnt bookkeeping sees the same pending loads on every trip and waits only
-//     for the step it consumes;
+//     (device_common.h) per tile, the step's scale metadata and its share of the step's
+//     activations into a register ring of DEPTH slots, so DEPTH-1 steps of weights are in
+//     flight while one is multiplied.  (A ring in LDS, filled by global_load_lds_dwordx4,
+//     would save the registers, but the compiler's wait-count insertion does not tell the
+//     slots of such a ring apart and waits for every pending copy before each LDS read.);
+//   * dense blocks load the activations four whole rows per instruction and pass them
+//     through a per-wave LDS tile into the MFMA operand layout (half the L1 cache-line
+//     requests of loading the operand layout directly); MoE blocks gather rows by route;
+//   * slots are compile-time indices (static_for), the loop body is branch-free, loads are
+//     issued in one fixed order on every path into the loop, so the compiler's vmcnt
+//     bookkeeping waits only for the step it consumes;
+//   * OCC = 3 instances fit three waves per SIMD (activations then run one step behind the
+//     weights, and the tiles are multiplied two at a time), so a launch of up to three
+//     workgroups per CU is resident in one round;
 //   * integer and fp8 weights use the integer-operand path (device_common.h): the MFMA B
 //     operand is the code itself and the scale / zero point is applied per group to the
 //     fp32 partial sums;
-//   * split-K across workgroups, when the grid needs it, and the epilogue are those of the
-//     tiled kernel (fp32 workspace, arrival counters, last arriver finishes).
+//   * K split across workgroups (when the grid needs it): the split blocks come first in
+//     the grid, add fp32 partial sums into a workspace with device-scope atomics, and the
+//     last arriver of a column group finishes it (arrival counters, as in gemm_kernel.h).
 #pragma once
 
 #include <type_traits>
