@@ -287,11 +287,12 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       return p;
     }
   }
-  // 16..64-row blocks: the multistage kernel (all of K's operands three steps ahead).
-  if (M <= 128 && env_int("MARLIN_MI355X_STREAM", 1) != 0) {
-    const int bm = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
+  // The multistage kernel (all of K's operands three steps ahead): 16..64-row blocks up to
+  // M = 128, 128-row blocks (one wave per SIMD, accumulators in AGPRs) beyond.
+  if (env_int("MARLIN_MI355X_STREAM", 1) != 0 && M <= env_int("MARLIN_MI355X_STREAM_MAX_M", 1 << 30)) {
+    const int bm = M <= 16 ? 16 : (M <= 32 ? 32 : (M <= 128 ? 64 : 128));
     int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
-    if (bm > 16 && nt == 1) nt = 0;  // not instantiated: fall through to the tiled kernel
+    if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
     nt = env_int("MARLIN_MI355X_STREAM_NT", nt);
     const bool small_meta_fits = !(kinds.gsm == GSM_SMALL && bm >= 48);
     if (nt > 0 && N % (64 * nt) == 0 && small_meta_fits) {
@@ -301,7 +302,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       p.stream = 1;
       p.m_blocks = (int)((M + bm - 1) / bm);
       p.n_blocks = (int)(N / (64 * nt));
-      p.xcd_group_m = 0;
+      p.xcd_group_m = env_int("MARLIN_MI355X_XCD_GROUP_M", bm >= 64 ? 4 : 0);
       GemmLaunch q = kinds;
       q.bm = bm;
       q.nt = nt;
@@ -772,6 +773,12 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     p.num_n_blocks = n_blocks;
     p.num_m_blocks = m_blocks;
     p.xcd_group_m = 0;
+    if (splits == 1) {
+      // moe blocks of one expert (and their activation rows) in one L2: groups of
+      // consecutive moe blocks x all column blocks dealt to the XCDs in turn
+      p.xcd_group_m = env_int("MARLIN_MI355X_MOE_GROUP_M", 4);
+      p.xcd_interleave = p.xcd_group_m > 0 ? 1 : 0;
+    }
     p.sorted_ids = sorted_token_ids;
     p.sorted_numel = (int)sorted_numel;
     p.expert_ids = expert_ids;

@@ -342,7 +342,10 @@ template <int FMT, class AT>
 struct IntOperand {
   static constexpr bool kEnabled = FMT == FMT_U4B8 || FMT == FMT_U4 || FMT == FMT_U8B128 ||
                                    FMT == FMT_U8 || FMT == FMT_FP8;
-  static constexpr bool kNeedRowSum = FMT != FMT_FP8;
+  // fp16 with a fixed code offset (uint4b8, uint8b128): one v_pk_add_f16 per register turns
+  // 1024+q into the signed value q-bias exactly, so the group sums need no row-sum term
+  static constexpr bool kDirect = AT::kId == 0 && (FMT == FMT_U4B8 || FMT == FMT_U8B128);
+  static constexpr bool kNeedRowSum = FMT != FMT_FP8 && !kDirect;
   // code offset carried by B: the magic number of the 16-bit pattern
   static constexpr float kMagic =
       (fmt_bits(FMT) == 4 || AT::kId == 0) ? (AT::kId == 0 ? 1024.0f : 128.0f) : 0.0f;
@@ -362,6 +365,8 @@ __device__ __forceinline__ IMeta make_imeta(MetaRaw raw) {
   const float s = raw16_to_float(raw.s & 0xffff, AT{});
   if constexpr (FMT == FMT_FP8) {
     return IMeta{s * 0.00390625f, 0.0f};
+  } else if constexpr (IO::kDirect) {
+    return IMeta{s, 0.0f};
   } else if constexpr (FMT == FMT_U4B8) {
     return IMeta{s, s * (IO::kMagic + 8.0f)};
   } else if constexpr (FMT == FMT_U8B128) {
@@ -416,6 +421,16 @@ __device__ __forceinline__ u32x4_t int_operand(uint32_t w0, uint32_t w1, uint32_
     r[1] = pack2((float)((w0 >> 16) & 0xffu), (float)(w0 >> 24), AT{});
     r[2] = pack2((float)(w1 & 0xffu), (float)((w1 >> 8) & 0xffu), AT{});
     r[3] = pack2((float)((w1 >> 16) & 0xffu), (float)(w1 >> 24), AT{});
+  }
+  if constexpr (IO::kDirect) {
+    constexpr _Float16 off = (_Float16)(-(IO::kMagic + (FMT == FMT_U4B8 ? 8.0f : 128.0f)));
+    // (each element goes through a scalar: __builtin_bit_cast of a vector element
+    // expression reads from the start of the vector)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = r[i];
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, x) + f16x2_t{off, off});
+    }
   }
   return r;
 }

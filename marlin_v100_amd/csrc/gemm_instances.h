@@ -64,6 +64,7 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     MMI_STREAM(32, 4, false)
     MMI_STREAM(64, 2, false)
     MMI_STREAM(64, 4, false)
+    MMI_STREAM(128, 4, false)
     MMI_STREAM(16, 4, true)
     MMI_STREAM(32, 4, true)
     MMI_STREAM(48, 4, true)

@@ -47,6 +47,7 @@ struct GemmParams {
   int num_n_blocks;
   int num_m_blocks;
   int xcd_group_m;  // m-blocks per group in the XCD-aware order (0: plain order)
+  int xcd_interleave;  // MoE: deal whole groups to the XCDs in turn (needs splits == 1)
   float* ws;
   int* counters;
   // MoE
@@ -104,11 +105,32 @@ __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)
 __device__ __forceinline__ void issue_order() { asm volatile("" ::: "memory"); }
 
 // Workgroup id -> (split, n block, m block).  Dense launches use the XCD-aware grouped
-// order when p.xcd_group_m > 0; MoE launches keep the plain order (one moe block per row).
+// order when p.xcd_group_m > 0: each XCD takes a contiguous range of the grouped order.
+// MoE launches with p.xcd_interleave set (splits == 1) deal whole groups (xcd_group_m moe
+// blocks x all n blocks) to the XCDs in turn: the moe blocks of one expert then share the
+// expert's weight slab, and the group's activation rows, in one L2, and the groups of dead
+// moe blocks at the end of the padded grid spread over all XCDs.
 __device__ __forceinline__ void decode_block(const GemmParams& p, int& split, int& n_blk,
                                              int& m_blk) {
   int id = blockIdx.x;
   const int total = gridDim.x;
+  if (p.xcd_interleave > 0) {
+    const int gm_full = p.xcd_group_m;
+    const int per_group = gm_full * p.num_n_blocks;
+    const int full = total - total % (kNumXcd * per_group);
+    if (id < full) {
+      const int j = id / kNumXcd;
+      id = ((j / per_group) * kNumXcd + id % kNumXcd) * per_group + j % per_group;
+    }
+    const int g = id / per_group;
+    const int first_m = g * gm_full;
+    const int gm = min(p.num_m_blocks - first_m, gm_full);
+    const int in = id - g * per_group;
+    split = 0;
+    m_blk = first_m + in % gm;
+    n_blk = in / gm;
+    return;
+  }
   if (p.xcd_group_m > 0) {
     const int full = total - total % kNumXcd;
     if (id < full) {

@@ -15,10 +15,11 @@
 //   * slots and buffers are compile-time indices (static_for), the loop body is
 //     branch-free, and prefetches past the last step are clamped to it, so the compiler's
 //     vmcnt bookkeeping is exact on every trip;
-//   * with at most two m-tiles, integer and fp8 weights with channelwise or >= 128-deep
-//     groups use the integer-operand path (device_common.h): codes feed the MFMA, the scale / zero point is applied per
-//     group to the fp32 partial sums; the 4-bit activation permutation it needs is applied
-//     once, by the wave that stages the fragment;
+//   * integer and fp8 weights with >= 128-deep groups (at most two m-tiles: the per-group
+//     partial sums cost registers) or channelwise scales (any tile) use the integer-operand
+//     path (device_common.h): codes feed the MFMA, the scale / zero point is applied to the
+//     fp32 sums; the 4-bit activation permutation it needs is applied once, by the wave
+//     that stages the fragment;
 //   * split-K, the XCD-aware block order, the MoE row gather / scatter and the epilogue are
 //     those of marlin_gemm_kernel (gemm_kernel.h).
 #pragma once
@@ -28,7 +29,7 @@
 namespace mmi {
 
 template <int FMT, class AT, int BM, int NT, int GSM, bool MOE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM >= 128 ? 1 : 2, 8)))
 void marlin_stream_kernel(const GemmParams p) {
   constexpr int MT = BM / 16;
   constexpr int BITS = fmt_bits(FMT);
@@ -40,7 +41,7 @@ void marlin_stream_kernel(const GemmParams p) {
   constexpr int D = 3;  // ring depth (register sets and LDS buffers)
   using IO = IntOperand<FMT, AT>;
   // (the per-group scaling keeps a second set of MT x NT accumulators: at most two m-tiles)
-  constexpr bool INT_B = IO::kEnabled && GSM != GSM_SMALL && MT <= 2;
+  constexpr bool INT_B = IO::kEnabled && GSM != GSM_SMALL && (MT <= 2 || GSM == GSM_CHANNEL);
   constexpr bool ROWSUM = INT_B && IO::kNeedRowSum;
 
   __shared__ u32x4_t lds_a0[FRAGS * 64];
