@@ -32,6 +32,7 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
 // Activation / output element tags.
@@ -433,6 +434,30 @@ __device__ __forceinline__ u32x4_t int_operand(uint32_t w0, uint32_t w1, uint32_
     }
   }
   return r;
+}
+
+// D += A(32x16) * B(16x32) (v_mfma_f32_32x32x16: twice the work of the 16x16x32 form in
+// about the same issue time on gfx950).  Lane l supplies A row l%32 / B column l%32,
+// k-slice 8*(l/32).  Result lane l holds D[8*(v/4) + 4*(l/32) + v%4][l%32], v = 0..15.
+__device__ __forceinline__ f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, f32x16_t c, F16) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, f32x16_t c, BF16) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Re-deals one word of two n16 tiles (x: tile t, y: tile t+1; 16-lane row g of a tile holds
+// k-slice g of a 32-deep block) into the B operands of two 32x32x16 MFMAs over the 32
+// columns: d0 = k-slices 0,1 (rows [x0, y0, x1, y1]), d1 = k-slices 2,3 ([x2, y2, x3, y3]).
+// v_permlane16_swap gives [x0, y0, x2, y2] / [x1, y1, x3, y3]; v_permlane32_swap of those
+// gives d0 / d1.
+__device__ __forceinline__ void deal32(uint32_t x, uint32_t y, uint32_t& d0, uint32_t& d1) {
+  const auto s16 = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+  const auto s32 = __builtin_amdgcn_permlane32_swap(s16[0], s16[1], false, false);
+  d0 = s32[0];
+  d1 = s32[1];
 }
 
 // D += A(16x32) * B(32x16).  Lane l supplies A row l%16 / B column l%16, k-slice 8*(l/16).

@@ -8,10 +8,12 @@
 //     1 KiB chunk), scale metadata and each wave's quarter of the activation tile are
 //     loaded into a ring of three register sets;
 //   * one step before use, each wave writes its quarter of the activation tile from the
-//     ring into one of three LDS buffers (fragment-major, so every A-operand ds_read_b128 is
-//     conflict-free); one barrier per step publishes it.  (Activations are not copied with
-//     global_load_lds_dwordx4: the compiler's wait-count insertion cannot tell the buffers of
-//     such a ring apart and would wait for every pending load before each LDS read.);
+//     ring into one of three LDS buffers (fragment-major with an XOR swizzle, so the staging
+//     writes and every A-operand ds_read_b128 are conflict-free); one barrier per step
+//     publishes it.  The quarter is loaded four whole rows per instruction.  (Activations
+//     are not copied with global_load_lds_dwordx4: the compiler's wait-count insertion
+//     cannot tell the buffers of such a ring apart and would wait for every pending load
+//     before each LDS read.);
 //   * slots and buffers are compile-time indices (static_for), the loop body is
 //     branch-free, and prefetches past the last step are clamped to it, so the compiler's
 //     vmcnt bookkeeping is exact on every trip;
@@ -40,8 +42,14 @@ void marlin_stream_kernel(const GemmParams p) {
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
   constexpr int D = 3;  // ring depth (register sets and LDS buffers)
   using IO = IntOperand<FMT, AT>;
-  // (the per-group scaling keeps a second set of MT x NT accumulators: at most two m-tiles)
-  constexpr bool INT_B = IO::kEnabled && GSM != GSM_SMALL && (MT <= 2 || GSM == GSM_CHANNEL);
+  // 32x32x16 MFMAs (full rate on gfx950) for blocks of >= 64 rows and tile pairs
+  constexpr bool M32 = BM >= 64 && NT % 2 == 0;
+  constexpr int MT32 = M32 ? BM / 32 : 1;
+  constexpr int NP = M32 ? NT / 2 : 1;
+  // (the per-group scaling keeps a second set of MT x NT accumulators: at most two m-tiles;
+  // the 32-row form has no room for row sums)
+  constexpr bool INT_B = IO::kEnabled && GSM != GSM_SMALL && (MT <= 2 || GSM == GSM_CHANNEL) &&
+                         !(M32 && IO::kNeedRowSum);
   constexpr bool ROWSUM = INT_B && IO::kNeedRowSum;
 
   __shared__ u32x4_t lds_a0[FRAGS * 64];
@@ -88,13 +96,19 @@ void marlin_stream_kernel(const GemmParams p) {
   }
   const int m0 = MOE ? 0 : m_blk * BM;
 
-  // Fragments staged by this wave: f = wave + 4*i covers k32 block f / MT, m16 tile f % MT.
+  // Activation staging: load i of this wave takes 16 bytes (8 k) at k offset 8*(lane%16) of
+  // block row 4*(wave*FPW + i) + lane/16, so one load covers four whole 256-byte rows of the
+  // step (8 full cache lines instead of 16 rows x 64 bytes).  Piece (row r, k chunk c) is
+  // MFMA fragment (block c/4, m16 tile r/16), entry (c%4)*16 + r%16, the entry's low four
+  // bits XOR-swizzled with c so that neither the 16 lanes writing one row nor the lanes
+  // reading one fragment collide on LDS banks.
+  auto a_unit = [&](int f, int g, int l16, int c) __attribute__((always_inline)) {
+    return f * 64 + g * 16 + (l16 ^ c);
+  };
   const uint16_t* a_src[FPW];
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
-    const int f = wave + 4 * i;
-    const int b = f / MT;
-    const int r = (f % MT) * 16 + ln;
+    const int r = (wave * FPW + i) * 4 + (lane >> 4);
     int64_t row;
     if constexpr (MOE) {
       const int id = lds_rows[r];
@@ -102,8 +116,13 @@ void marlin_stream_kernel(const GemmParams p) {
     } else {
       row = min(m0 + r, p.M - 1);
     }
-    a_src[i] = a + row * p.a_stride + 32 * b + 8 * lg;
+    a_src[i] = a + row * p.a_stride + 8 * (lane & 15);
   }
+  auto stage_unit = [&](int i) __attribute__((always_inline)) {
+    const int r = (wave * FPW + i) * 4 + (lane >> 4);
+    const int c = lane & 15;
+    return a_unit((c >> 2) * MT + (r >> 4), c & 3, r & 15, c);
+  };
 
   const int tn0 = n_blk * (BN / 16) + wave * NT;
   const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
@@ -121,6 +140,12 @@ void marlin_stream_kernel(const GemmParams p) {
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x16_t acc32[MT32][NP];
+#pragma unroll
+  for (int i = 0; i < MT32; ++i)
+#pragma unroll
+    for (int t = 0; t < NP; ++t) acc32[i][t] = f32x16_t{};
+  const int hi = (lane >> 4) & 1;  // M32: which tile of a pair holds this lane's column
   f32x4_t rsum[MT];  // channelwise integer-operand path: row sums over all of K
 #pragma unroll
   for (int i = 0; i < MT; ++i) rsum[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -167,10 +192,8 @@ void marlin_stream_kernel(const GemmParams p) {
     constexpr int d = decltype(dc)::value;
     Buf& lb = buf(dc);
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) {
-      const int f = wave + 4 * i;
-      lb[f * 64 + lane] = (INT_B && BITS == 4) ? a_perm_u4(ra[d][i]) : ra[d][i];
-    }
+    for (int i = 0; i < FPW; ++i)
+      lb[stage_unit(i)] = (INT_B && BITS == 4) ? a_perm_u4(ra[d][i]) : ra[d][i];
   };
 
   auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) __attribute__((always_inline)) {
@@ -186,7 +209,47 @@ void marlin_stream_kernel(const GemmParams p) {
   // Multiply one step: activations from LDS buffer lb, weights / metadata from registers.
   auto compute_core = [&](const Buf& lb, const u32x4_t (&bv)[NT][NL],
                           const MetaRaw (&mv)[NT][RAWB], int nblocks) __attribute__((always_inline)) {
-    if constexpr (INT_B) {
+    if constexpr (M32) {
+      // 32-row A operands straight from the 16x16 fragments (rows 32I + l%32, k-slice
+      // 2h + l/32 of block b); B operands re-dealt from tile pairs with deal32().
+      Meta mm[NP];
+      if constexpr (!INT_B) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          if constexpr (GSM == GSM_CHANNEL) mm[q] = hi ? meta_ch[2 * q + 1] : meta_ch[2 * q];
+          else mm[q] = make_meta<FMT, AT>(hi ? mv[2 * q + 1][0] : mv[2 * q][0]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (b < nblocks) {
+          u32x4_t a32[MT32][2];
+#pragma unroll
+          for (int i = 0; i < MT32; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              a32[i][h] = lb[a_unit(b * MT + 2 * i + hi, 2 * h + (lane >> 5), lane & 15,
+                                    4 * b + 2 * h + (lane >> 5))];
+#pragma unroll
+          for (int q = 0; q < NP; ++q) {
+            uint32_t x0, x1, y0, y1;
+            b_words(bv, 2 * q, b, x0, x1);
+            b_words(bv, 2 * q + 1, b, y0, y1);
+            uint32_t w0[2], w1[2] = {0u, 0u};
+            deal32(x0, y0, w0[0], w0[1]);
+            if constexpr (BITS == 8) deal32(x1, y1, w1[0], w1[1]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              u32x4_t bop;
+              if constexpr (INT_B) bop = int_operand<FMT, AT>(w0[h], w1[h], vz);
+              else bop = dequant_operand<FMT, AT>(w0[h], w1[h], mm[q], vz);
+#pragma unroll
+              for (int i = 0; i < MT32; ++i) acc32[i][q] = mfma32(a32[i][h], bop, acc32[i][q], AT{});
+            }
+          }
+        }
+      }
+    } else if constexpr (INT_B) {
       f32x4_t d[MT][NT];
       f32x4_t r[MT];
 #pragma unroll
@@ -202,7 +265,7 @@ void marlin_stream_kernel(const GemmParams p) {
         if (b < nblocks) {
           u32x4_t af[MT];
 #pragma unroll
-          for (int i = 0; i < MT; ++i) af[i] = lb[(b * MT + i) * 64 + lane];
+          for (int i = 0; i < MT; ++i) af[i] = lb[a_unit(b * MT + i, lg, ln, 4 * b + lg)];
           if constexpr (ROWSUM) {
 #pragma unroll
             for (int i = 0; i < MT; ++i) r[i] = mfma16(af[i], ones, r[i], AT{});
@@ -256,7 +319,7 @@ void marlin_stream_kernel(const GemmParams p) {
           }
           u32x4_t af[MT];
 #pragma unroll
-          for (int i = 0; i < MT; ++i) af[i] = lb[(b * MT + i) * 64 + lane];
+          for (int i = 0; i < MT; ++i) af[i] = lb[a_unit(b * MT + i, lg, ln, 4 * b + lg)];
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
             uint32_t w0, w1;
@@ -308,11 +371,10 @@ void marlin_stream_kernel(const GemmParams p) {
     const int kt0 = total_full * 128;
 #pragma unroll
     for (int i = 0; i < FPW; ++i) {
-      const int f = wave + 4 * i;
-      const int b = f / MT;
+      const int b = (lane & 15) >> 2;
       u32x4_t v = b < nblocks ? *reinterpret_cast<const u32x4_t*>(a_src[i] + kt0)
                               : u32x4_t{0u, 0u, 0u, 0u};
-      lds_a2[f * 64 + lane] = (INT_B && BITS == 4) ? a_perm_u4(v) : v;
+      lds_a2[stage_unit(i)] = (INT_B && BITS == 4) ? a_perm_u4(v) : v;
     }
     u32x4_t bw[NT][NL];
     MetaRaw raw[NT][RAWB];
@@ -347,7 +409,16 @@ void marlin_stream_kernel(const GemmParams p) {
     compute_core(lds_a2, bw, raw, nblocks);
   }
 
-  if constexpr (INT_B && GSM == GSM_CHANNEL) {
+  if constexpr (INT_B && GSM == GSM_CHANNEL && M32) {
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + 2 * q + hi) * 16 + ln));
+#pragma unroll
+      for (int i = 0; i < MT32; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc32[i][q][v] *= m.S;
+    }
+  } else if constexpr (INT_B && GSM == GSM_CHANNEL) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
@@ -394,29 +465,38 @@ void marlin_stream_kernel(const GemmParams p) {
     cout[orow * p.N + col] = to_raw16(o, AT{});
   };
 
+  // every output this lane holds: (block row, column, value)
+  auto for_out = [&](auto&& f) __attribute__((always_inline)) {
+    if constexpr (M32) {
+#pragma unroll
+      for (int i = 0; i < MT32; ++i)
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            f(32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3), (tn0 + 2 * q) * 16 + (lane & 31),
+              acc32[i][q][v]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) f(i * 16 + lg * 4 + e, (tn0 + t) * 16 + ln, acc[i][t][e]);
+    }
+  };
+
   if (p.splits == 1) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          finish(i * 16 + lg * 4 + e, (tn0 + t) * 16 + ln, acc[i][t][e]);
+    for_out([&](int r, int col, float v) __attribute__((always_inline)) { finish(r, col, v); });
     return;
   }
 
   // split-K (same protocol as marlin_gemm_kernel)
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t orow = out_row(i * 16 + lg * 4 + e);
-        if (orow >= 0)
-          __hip_atomic_fetch_add(p.ws + orow * p.N + (tn0 + t) * 16 + ln, acc[i][t][e],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+  for_out([&](int r, int col, float v) __attribute__((always_inline)) {
+    const int64_t orow = out_row(r);
+    if (orow >= 0)
+      __hip_atomic_fetch_add(p.ws + orow * p.N + col, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  });
   wait_vm_all();
   __syncthreads();
   if (tid == 0) {
@@ -426,21 +506,14 @@ void marlin_stream_kernel(const GemmParams p) {
   }
   __syncthreads();
   if (!lds_last) return;
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = i * 16 + lg * 4 + e;
-        const int64_t orow = out_row(r);
-        if (orow >= 0) {
-          const int col = (tn0 + t) * 16 + ln;
-          const float v = __hip_atomic_exchange(p.ws + orow * p.N + col, 0.0f, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-          finish(r, col, v);
-        }
-      }
+  for_out([&](int r, int col, float) __attribute__((always_inline)) {
+    const int64_t orow = out_row(r);
+    if (orow >= 0) {
+      const float v = __hip_atomic_exchange(p.ws + orow * p.N + col, 0.0f, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+      finish(r, col, v);
+    }
+  });
   if (tid == 0)
     __hip_atomic_store(p.counters + out_tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
