@@ -191,6 +191,16 @@ marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t 
                                int64_t top_k, int64_t hidden, void* out,
                                marlin_stream_t stream);
 
+/*
+ * MoE SiLU-gated activation: out[r, j] = silu(input[r, j]) * input[r, d + j] for an input of
+ * shape [rows, 2d] and an output of shape [rows, d], both contiguous; silu is rounded to the
+ * element type before the product, as the reference's torch expression does.
+ * Replaces the SiLU branch of apply_moe_activation
+ * (reference vllm/model_executor/layers/fused_moe/activation.py:45-52).
+ */
+marlin_status_t marlin_silu_and_mul(const void* input, marlin_dtype_t dtype, int64_t rows,
+                                    int64_t d, void* out, marlin_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

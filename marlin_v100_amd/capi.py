@@ -49,6 +49,7 @@ SIGNATURES = {
     "marlin_dequantize": (_I, [_P, _I64, _P, _I, _I64, _I64, _P, _I, _I64, _P, _I64, _I64, _I64,
                                _I64, _I, _P, _P]),
     "marlin_moe_sum": (_I, [_P, _I, _I64, _I64, _I64, _P, _P]),
+    "marlin_silu_and_mul": (_I, [_P, _I, _I64, _I64, _P, _P]),
 }
 
 _lib = None
@@ -173,4 +174,12 @@ def dequantize(b_q_weight, b_scales, b_type_id, size_k, size_n, out_dtype, *, b_
 def moe_sum(inp, out):
     _check(load().marlin_moe_sum(_ptr(inp), _dt(inp), inp.shape[0], inp.shape[1], inp.shape[2],
                                  _ptr(out), _stream()))
+    return out
+
+
+def silu_and_mul(out, x):
+    """out[r, :] = silu(x[r, :d]) * x[r, d:] for contiguous x [rows, 2d], out [rows, d]."""
+    d = x.shape[-1] // 2
+    rows = x.numel() // max(2 * d, 1)
+    _check(load().marlin_silu_and_mul(_ptr(x), _dt(x), rows, d, _ptr(out), _stream()))
     return out

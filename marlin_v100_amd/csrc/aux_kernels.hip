@@ -1,4 +1,7 @@
-// aux_kernels.hip -- dequantize (inspection op), moe_align_block_size and moe_sum.
+// aux_kernels.hip -- dequantize (inspection op), moe_align_block_size, moe_sum and the MoE
+// SiLU-and-multiply activation.
+#include <algorithm>
+
 #include "gemm_kernel.h"
 #include "host_common.h"
 
@@ -214,6 +217,69 @@ hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, i
   else
     hipLaunchKernelGGL((moe_sum_kernel<F16>), grid, dim3(256), 0, stream, i16, o16, tokens, topk,
                        hidden);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
+// silu_and_mul: out[r, j] = silu(x[r, j]) * x[r, d + j], rounded as the reference's torch
+// expression F.silu(gate) * up rounds: silu to the element type, then the product.
+// ---------------------------------------------------------------------------------------
+template <class AT>
+__device__ __forceinline__ float silu_mul1(uint32_t g_raw, uint32_t u_raw) {
+  const float g = raw16_to_float(g_raw & 0xffffu, AT{});
+  const float u = raw16_to_float(u_raw & 0xffffu, AT{});
+  const float s = raw16_to_float(to_raw16(g / (1.0f + expf(-g)), AT{}), AT{});
+  return s * u;
+}
+
+// d % 8 == 0: 8 outputs (16 bytes) per thread
+template <class AT>
+__global__ void silu_mul_kernel_v8(const uint16_t* __restrict__ x, uint16_t* __restrict__ out,
+                                   int64_t rows, int64_t d) {
+  const int64_t per_row = d >> 3;
+  const int64_t n = rows * per_row;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / per_row;
+    const int64_t c = (i - r * per_row) * 8;
+    const u32x4_t g = *reinterpret_cast<const u32x4_t*>(x + r * 2 * d + c);
+    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(x + r * 2 * d + d + c);
+    u32x4_t o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      o[w] = pack2(silu_mul1<AT>(g[w], u[w]), silu_mul1<AT>(g[w] >> 16, u[w] >> 16), AT{});
+    *reinterpret_cast<u32x4_t*>(out + r * d + c) = o;
+  }
+}
+
+template <class AT>
+__global__ void silu_mul_kernel_v1(const uint16_t* __restrict__ x, uint16_t* __restrict__ out,
+                                   int64_t rows, int64_t d) {
+  const int64_t n = rows * d;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / d;
+    const int64_t c = i - r * d;
+    out[i] = to_raw16(silu_mul1<AT>(x[r * 2 * d + c], x[r * 2 * d + d + c]), AT{});
+  }
+}
+
+hipError_t launch_silu_and_mul(const void* x, bool bf16, int64_t rows, int64_t d, void* out,
+                               hipStream_t stream) {
+  if (rows == 0 || d == 0) return hipSuccess;
+  const uint16_t* x16 = reinterpret_cast<const uint16_t*>(x);
+  uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
+  const bool v8 = d % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  const int64_t work = v8 ? rows * (d / 8) : rows * d;
+  const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 8192);
+  if (v8) {
+    if (bf16) hipLaunchKernelGGL((silu_mul_kernel_v8<BF16>), dim3(grid), dim3(256), 0, stream, x16, o16, rows, d);
+    else hipLaunchKernelGGL((silu_mul_kernel_v8<F16>), dim3(grid), dim3(256), 0, stream, x16, o16, rows, d);
+  } else {
+    if (bf16) hipLaunchKernelGGL((silu_mul_kernel_v1<BF16>), dim3(grid), dim3(256), 0, stream, x16, o16, rows, d);
+    else hipLaunchKernelGGL((silu_mul_kernel_v1<F16>), dim3(grid), dim3(256), 0, stream, x16, o16, rows, d);
+  }
   return hipGetLastError();
 }
 

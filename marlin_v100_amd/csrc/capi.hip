@@ -879,4 +879,17 @@ marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t 
   });
 }
 
+marlin_status_t marlin_silu_and_mul(const void* input, marlin_dtype_t dtype, int64_t rows,
+                                    int64_t d, void* out, marlin_stream_t stream) {
+  return guarded([&] {
+    check(is_half_type(dtype), "silu_and_mul supports float16 and bfloat16");
+    check(rows >= 0 && d >= 0, "invalid silu_and_mul shape");
+    if (rows == 0 || d == 0) return;
+    check(input && out, "null tensor pointer");
+    check_hip(launch_silu_and_mul(input, dtype == MARLIN_DTYPE_BFLOAT16, rows, d, out,
+                                  (hipStream_t)stream),
+              "silu_and_mul launch");
+  });
+}
+
 }  // extern "C"

@@ -20,6 +20,8 @@ hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, in
 hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, int bs, int* sorted,
                             int64_t sorted_numel, int* expert_ids, int64_t expert_ids_numel,
                             int* post_pad, const int* expert_map, hipStream_t stream);
+hipError_t launch_silu_and_mul(const void* x, bool bf16, int64_t rows, int64_t d, void* out,
+                               hipStream_t stream);
 hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, int64_t hidden,
                           void* out, hipStream_t stream);
 

@@ -42,8 +42,10 @@ void marlin_stream_kernel(const GemmParams p) {
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
   constexpr int D = 3;  // ring depth (register sets and LDS buffers)
   using IO = IntOperand<FMT, AT>;
-  // 32x32x16 MFMAs (full rate on gfx950) for blocks of >= 64 rows and tile pairs
-  constexpr bool M32 = BM >= 64 && NT % 2 == 0;
+  // 32x32x16 MFMAs (full rate on gfx950) for 128-row blocks and tile pairs; they also stage
+  // the activations line by line (below).  Smaller blocks keep the 16x16x32 form and the
+  // fragment-ordered loads, whose LDS addressing costs fewer registers at two waves per SIMD.
+  constexpr bool M32 = BM >= 128 && NT % 2 == 0;
   constexpr int MT32 = M32 ? BM / 32 : 1;
   constexpr int NP = M32 ? NT / 2 : 1;
   // (the per-group scaling keeps a second set of MT x NT accumulators: at most two m-tiles;
@@ -103,12 +105,14 @@ void marlin_stream_kernel(const GemmParams p) {
   // bits XOR-swizzled with c so that neither the 16 lanes writing one row nor the lanes
   // reading one fragment collide on LDS banks.
   auto a_unit = [&](int f, int g, int l16, int c) __attribute__((always_inline)) {
-    return f * 64 + g * 16 + (l16 ^ c);
+    return M32 ? f * 64 + g * 16 + (l16 ^ c) : f * 64 + g * 16 + l16;
   };
   const uint16_t* a_src[FPW];
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
-    const int r = (wave * FPW + i) * 4 + (lane >> 4);
+    // (16x16 form: fragment f = wave + 4*i, k32 block f / MT, m16 tile f % MT, 16 rows x
+    // 64 bytes per load)
+    const int r = M32 ? (wave * FPW + i) * 4 + (lane >> 4) : ((wave + 4 * i) % MT) * 16 + ln;
     int64_t row;
     if constexpr (MOE) {
       const int id = lds_rows[r];
@@ -116,12 +120,16 @@ void marlin_stream_kernel(const GemmParams p) {
     } else {
       row = min(m0 + r, p.M - 1);
     }
-    a_src[i] = a + row * p.a_stride + 8 * (lane & 15);
+    a_src[i] = a + row * p.a_stride + (M32 ? 8 * (lane & 15) : 32 * ((wave + 4 * i) / MT) + 8 * lg);
   }
   auto stage_unit = [&](int i) __attribute__((always_inline)) {
-    const int r = (wave * FPW + i) * 4 + (lane >> 4);
-    const int c = lane & 15;
-    return a_unit((c >> 2) * MT + (r >> 4), c & 3, r & 15, c);
+    if constexpr (M32) {
+      const int r = (wave * FPW + i) * 4 + (lane >> 4);
+      const int c = lane & 15;
+      return a_unit((c >> 2) * MT + (r >> 4), c & 3, r & 15, c);
+    } else {
+      return (wave + 4 * i) * 64 + lane;
+    }
   };
 
   const int tn0 = n_blk * (BN / 16) + wave * NT;
@@ -371,7 +379,7 @@ void marlin_stream_kernel(const GemmParams p) {
     const int kt0 = total_full * 128;
 #pragma unroll
     for (int i = 0; i < FPW; ++i) {
-      const int b = (lane & 15) >> 2;
+      const int b = M32 ? (lane & 15) >> 2 : (wave + 4 * i) / MT;
       u32x4_t v = b < nblocks ? *reinterpret_cast<const u32x4_t*>(a_src[i] + kt0)
                               : u32x4_t{0u, 0u, 0u, 0u};
       lds_a2[stage_unit(i)] = (INT_B && BITS == 4) ? a_perm_u4(v) : v;

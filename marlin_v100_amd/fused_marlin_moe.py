@@ -39,8 +39,10 @@ def select_block_size_m(m: int, topk: int, num_experts: int) -> int:
 
 
 def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
-    d = x.shape[-1] // 2
-    torch.mul(torch.nn.functional.silu(x[..., :d]), x[..., d:], out=out)
+    """out = silu(x[..., :d]) * x[..., d:] (activation.py:45-52) in one native pass."""
+    from . import capi
+
+    capi.silu_and_mul(out, x.contiguous())
 
 
 def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,

@@ -129,3 +129,22 @@ def test_fused_marlin_moe_layer(dtype):
                            is_w2_zp_float=True).cpu()
     ref = O.moe_layer_ref(x, d13, d2, tw, ids)
     assert O.max_abs_rel_err(out, ref) <= 2 * TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,d", [(64, 1536), (7, 24), (5, 12), (0, 16)])
+def test_silu_and_mul(dtype, rows, d):
+    """Native activation vs the reference expression F.silu(gate) * up in the element type
+    (activation.py:45-52): silu rounded to the element type, then the product."""
+    gen = torch.Generator().manual_seed(rows * 131 + d)
+    x = (torch.randn((rows, 2 * d), generator=gen) * 3).to(dtype)
+    out = torch.empty((rows, d), dtype=dtype, device="cuda")
+    capi.silu_and_mul(out, x.cuda())
+    g, u = x[:, :d].float(), x[:, d:].float()
+    ref = (torch.nn.functional.silu(g).to(dtype).float() * u).to(dtype)
+    got = out.cpu()
+    if rows == 0:
+        return
+    assert O.max_abs_rel_err(got, ref) <= 1e-2
+    exact = (got.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
+    assert exact >= 0.99, exact
