@@ -202,7 +202,8 @@ int env_int(const char* name, int dflt) {
 //    resident in one round -- a second, partial round would stream its weights alone at the
 //    end -- and spread evenly over the CUs: each CU takes the same number of whole column
 //    groups and the groups left over are split along K into about one small block per CU.
-//    With fewer groups than CUs, K is split across blocks within an atomics budget.
+//    With at most half as many 64-column groups as CUs the groups are 32 columns wide; K is split across
+//    blocks only when under a quarter of the CUs would have a group, within an atomics budget.
 //  * 16 < M <= 32 is still weight bound: 32-row blocks with split-K until the grid holds
 //    about 4 workgroups per CU.
 //  * Larger M is MFMA bound: 64x256 or 128x256 blocks (each wave 64/128 x 64) visited in the
@@ -219,6 +220,10 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
   if (M <= 16) {
     int nt = int_operand ? 4 : 2, depth = int_operand ? 3 : 4, wpb = 4, ksplit = 1,
         occ = int_operand ? 3 : 1;
+    // at most half as many 64-column groups as CUs: 32-column groups instead (twice the
+    // workgroups, no cross-workgroup split; cfg1 4096x4096: 6.9 us against 12.7 us with
+    // split K; N = 14336, 224 groups, stays at 64 columns: 9.5 against 11.9 us)
+    if (int_operand && N / 64 <= cus / 2) nt = 2, depth = 4, occ = 1;
     if (const char* t = getenv("MARLIN_MI355X_DECODE")) {
       sscanf(t, "%d,%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit, &occ);
     } else if (occ == 3) {
@@ -267,13 +272,14 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
           splits = std::max(splits, 1);
         }
         if (splits == 1) main_blocks = 0;
-      } else if (blocks_n < resident) {
-        // fewer groups than CUs: split K across blocks, as far as the device-scope atomics
-        // of the partial sums stay cheap (about 256K of them per call)
+      } else if (blocks_n * 4 <= cus) {
+        // far fewer groups than CUs: split K across blocks, as far as the device-scope
+        // atomics of the partial sums stay cheap (about 64K per call; measured: splitting
+        // cost more than it gained whenever a quarter of the CUs or more had a group)
         const int min_steps = 2 * (ksplit ? wpb : 1);  // per split
         if (steps >= 2 * min_steps)
           splits = (int)std::min<int64_t>(resident / blocks_n, steps / min_steps);
-        const int64_t budget = std::max<int64_t>(1, (int64_t(1) << 18) / std::max<int64_t>(M * N, 1));
+        const int64_t budget = std::max<int64_t>(1, (int64_t(1) << 16) / std::max<int64_t>(M * N, 1));
         splits = (int)std::min<int64_t>(splits, budget);
         splits = std::max(splits, 1);
       }
