@@ -298,7 +298,12 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
   // The multistage kernel (all of K's operands three steps ahead): 16..64-row blocks up to
   // M = 128, 128-row blocks (one wave per SIMD, accumulators in AGPRs) beyond.
   if (env_int("MARLIN_MI355X_STREAM", 1) != 0 && M <= env_int("MARLIN_MI355X_STREAM_MAX_M", 1 << 30)) {
-    const int bm = M <= 16 ? 16 : (M <= 32 ? 32 : (M <= 128 ? 64 : 128));
+    int bm = M <= 16 ? 16 : (M <= 32 ? 32 : (M <= 128 ? 64 : 128));
+    // per-32/16 group metadata for 48+ rows does not fit the register budget: 32-row blocks
+    // up to M = 1024, the tiled kernel beyond (measured on cfg4 MXFP4: 35 / 75 / 252 us at
+    // M = 64 / 512 / 2048 against 47 / 184 / 211 us tiled)
+    if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= env_int("MARLIN_MI355X_SMALL_GROUP_MAX_M", 1024))
+      bm = 32;
     int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
     if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
     nt = env_int("MARLIN_MI355X_STREAM_NT", nt);
