@@ -73,102 +73,183 @@ hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, in
 // ---------------------------------------------------------------------------------------
 // moe_align_block_size (reference moe_align_sum_kernels.cu:81-181, 291-320), one workgroup
 // of 1024 threads.  Unlike the reference's atomic scatter, placement is deterministic:
-// route indices of one expert appear in ascending order.  Rounds of 1024 indices are placed
-// in index order; inside a round each wavefront ranks its lanes per expert with one ballot
-// per expert-id bit and wavefronts are ordered by a per-expert prefix over per-wave counts
-// kept in LDS.
+// route indices of one expert appear in ascending order.
+//   * Routes are ranked in rounds of 16 x 1024 indices: wavefront w of a round takes 1024
+//     consecutive indices in 16 passes of 64, ranks its lanes per expert with one ballot
+//     per expert-id bit (plus the expert's count from the wavefront's earlier passes, kept
+//     in LDS), and wavefronts are ordered by a per-expert prefix over the per-wave counts.
+//   * Up to 16K routes (T = 2048 tokens at top-8) that one round is also the histogram: the
+//     topk ids are read once, ranks stay in registers across the scan.  Larger inputs count
+//     first (one LDS atomic per expert and wavefront pass), then rank and place round by
+//     round.
+//   * The padded prefix is a wavefront shuffle scan plus one cross-wave step.  The topk ids
+//     of all 16 passes are loaded before any is inspected.
 // ---------------------------------------------------------------------------------------
+constexpr int kAlignPasses = 16;  // passes of 64 routes per wavefront per round
+
 template <typename IdT>
 __global__ __launch_bounds__(1024) void moe_align_kernel(
     const IdT* __restrict__ topk, int64_t numel, int E, int bs, int* __restrict__ sorted,
     int64_t sorted_numel, int* __restrict__ expert_ids, int64_t expert_ids_numel,
     int* __restrict__ post_pad, const int* __restrict__ expert_map, int has_map) {
   extern __shared__ int smem[];
-  int* counts = smem;             // [E]
-  int* cursor = counts + E;       // [E + 1] exclusive padded prefix, then running cursor
-  uint8_t* wave_cnt = reinterpret_cast<uint8_t*>(cursor + E + 1);  // [16][E]
-  __shared__ int scan_tmp[1024];
+  int* counts = smem;        // [E] routes per expert (whole input)
+  int* cursor = counts + E;  // [E + 1] padded exclusive prefix, advanced round by round
+  int* round_n = cursor + E + 1;  // [E] routes per expert in the current round
+  // [16][E] per wave and expert: routes so far in this round, then the exclusive prefix over
+  // the waves (both < 16 * 1024, so 16 bits suffice)
+  uint16_t* wave_cnt = reinterpret_cast<uint16_t*>(round_n + E);
+  __shared__ int wave_sum[16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int ebits = E > 1 ? 32 - __clz(E - 1) : 1;  // bits of the largest expert id
+  const uint64_t lanes_below = (1ull << lane) - 1;
+  constexpr int64_t kRound = 1024 * kAlignPasses;
 
-  auto mapped = [&](int64_t i) -> int {
-    int64_t e = (int64_t)topk[i];
-    if (e < 0 || e >= E) return -1;
-    int me = (int)e;
-    if (has_map) {
-      me = expert_map[me];
-      if (me < 0 || me >= E) return -1;
+  // Expert of routes wbase + 64 s + lane, s < kAlignPasses (-1: none or invalid).  Every
+  // pass's id is loaded before any is inspected (clamped indices, no branch between the
+  // loads), then the expert_map lookups likewise, so the loads overlap.
+  auto load_experts = [&](int64_t wbase, int (&ev)[kAlignPasses]) {
+    const int64_t last = numel > 0 ? numel - 1 : 0;
+    // passes that hold routes (wave-uniform)
+    const int live = (int)max<int64_t>(0, min<int64_t>(kAlignPasses, (numel - wbase + 63) / 64));
+    int64_t raw[kAlignPasses];
+#pragma unroll
+    for (int s = 0; s < kAlignPasses; ++s)
+      raw[s] = s < live ? (int64_t)topk[min(wbase + s * 64 + lane, last)] : -1;
+#pragma unroll
+    for (int s = 0; s < kAlignPasses; ++s) {
+      const bool ok = wbase + s * 64 + lane < numel && raw[s] >= 0 && raw[s] < E;
+      ev[s] = ok ? (int)raw[s] : -1;
     }
-    return me;
+    if (has_map) {
+      int me[kAlignPasses];
+#pragma unroll
+      for (int s = 0; s < kAlignPasses; ++s) me[s] = expert_map[ev[s] >= 0 ? ev[s] : 0];
+#pragma unroll
+      for (int s = 0; s < kAlignPasses; ++s)
+        ev[s] = (ev[s] >= 0 && me[s] >= 0 && me[s] < E) ? me[s] : -1;
+    }
   };
-
-  for (int e = tid; e < E; e += 1024) counts[e] = 0;
-  __syncthreads();
-  for (int64_t i = tid; i < numel; i += 1024) {
-    const int e = mapped(i);
-    if (e >= 0) atomicAdd(&counts[e], 1);
-  }
-  __syncthreads();
-
-  // exclusive scan of padded counts (E <= 1024: one value per thread)
-  int v = 0;
-  if (tid < E) v = (counts[tid] + bs - 1) / bs * bs;
-  scan_tmp[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int add = tid >= off ? scan_tmp[tid - off] : 0;
-    __syncthreads();
-    scan_tmp[tid] += add;
-    __syncthreads();
-  }
-  const int incl = scan_tmp[tid];
-  if (tid < E) cursor[tid] = incl - v;
-  if (tid == E - 1) cursor[E] = incl;
-  __syncthreads();
-  const int total = cursor[E];
-  if (tid == 0) post_pad[0] = total;
-
-  // expert_ids
-  for (int e = tid; e < E; e += 1024) {
-    for (int b = cursor[e] / bs; b < cursor[e + 1] / bs; ++b)
-      if (b < expert_ids_numel) expert_ids[b] = e;
-  }
-  for (int64_t b = total / bs + tid; b < expert_ids_numel; b += 1024) expert_ids[b] = -1;
-
-  // sentinel fill, then placement
-  for (int64_t i = tid; i < sorted_numel; i += 1024) sorted[i] = (int)numel;
-  __syncthreads();
-
-  for (int64_t base = 0; base < numel; base += 1024) {
-    const int64_t i = base + tid;
-    const int e = i < numel ? mapped(i) : -1;
-    for (int x = lane; x < E; x += 64) wave_cnt[wave * E + x] = 0;
-    // lanes holding the same expert: intersect, over the id's bits, the ballots that agree
-    // with this lane's bit (no per-expert loop)
+  // lanes of this wave holding the same expert as this lane: intersect, over the id's bits,
+  // the ballots that agree with this lane's bit (no per-expert loop)
+  auto same_expert = [&](int e) -> uint64_t {
     uint64_t same = __ballot(e >= 0);
     for (int bit = 0; bit < ebits; ++bit) {
       const int set = (e >> bit) & 1;
       const uint64_t m = __ballot(set);
       same &= set ? m : ~m;
     }
-    const uint64_t before = same & ((1ull << lane) - 1);
-    const int rank = __popcll(before);
-    if (e >= 0 && before == 0) wave_cnt[wave * E + e] = (uint8_t)__popcll(same);
-    __syncthreads();
-    if (e >= 0) {
-      int pos = cursor[e] + rank;
-      for (int w = 0; w < wave; ++w) pos += wave_cnt[w * E + e];
-      if (pos < sorted_numel) sorted[pos] = (int)i;
+    return same;
+  };
+
+  // Rank the round starting at `base`: ex / rk get each pass's expert and its rank among
+  // the wave's routes of that expert; then wave_cnt holds the wave-exclusive prefix and
+  // round_n the round's count per expert.
+  int ex[kAlignPasses], rk[kAlignPasses];
+  auto rank_round = [&](int64_t base) {
+    const int64_t wbase = base + (int64_t)wave * 64 * kAlignPasses;
+    for (int x = lane; x < E; x += 64) wave_cnt[wave * E + x] = 0;  // this wave's row only
+    load_experts(wbase, ex);
+#pragma unroll
+    for (int s = 0; s < kAlignPasses; ++s) {
+      rk[s] = 0;
+      if (wbase + s * 64 >= numel) continue;  // wave-uniform: passes past the end
+      const int e = ex[s];
+      const uint64_t same = same_expert(e);
+      const uint64_t before = same & lanes_below;
+      int r = 0;
+      if (e >= 0) r = wave_cnt[wave * E + e] + __popcll(before);
+      // the leader's store depends on its own read, so every lane of the wave has read the
+      // old count before it lands
+      if (e >= 0 && before == 0) wave_cnt[wave * E + e] = (uint16_t)(r + __popcll(same));
+      rk[s] = r;
     }
     __syncthreads();
     for (int x = tid; x < E; x += 1024) {
-      int add = 0;
-      for (int w = 0; w < 16; ++w) add += wave_cnt[w * E + x];
-      cursor[x] += add;
+      int run = 0;
+      for (int w = 0; w < 16; ++w) {
+        const int c = wave_cnt[w * E + x];
+        wave_cnt[w * E + x] = (uint16_t)run;
+        run += c;
+      }
+      round_n[x] = run;
     }
+    __syncthreads();
+  };
+  auto place_round = [&](int64_t base) {
+    const int64_t wbase = base + (int64_t)wave * 64 * kAlignPasses;
+#pragma unroll
+    for (int s = 0; s < kAlignPasses; ++s) {
+      const int e = ex[s];
+      if (e >= 0) {
+        const int pos = cursor[e] + wave_cnt[wave * E + e] + rk[s];
+        if (pos < sorted_numel) sorted[pos] = (int)(wbase + s * 64 + lane);
+      }
+    }
+  };
+
+  // sentinels everywhere first (coalesced; placement overwrites the route slots after the
+  // barriers below, which also wait for these stores)
+  for (int64_t j = tid; j < sorted_numel; j += 1024) sorted[j] = (int)numel;
+
+  const bool one_round = numel <= kRound;
+  if (one_round) {
+    rank_round(0);
+    for (int x = tid; x < E; x += 1024) counts[x] = round_n[x];
+  } else {
+    for (int x = tid; x < E; x += 1024) counts[x] = 0;
+    __syncthreads();
+    for (int64_t base = 0; base < numel; base += kRound) {
+      const int64_t wbase = base + (int64_t)wave * 64 * kAlignPasses;
+      int ev[kAlignPasses];
+      load_experts(wbase, ev);
+#pragma unroll
+      for (int s = 0; s < kAlignPasses; ++s) {
+        if (wbase + s * 64 >= numel) continue;
+        const uint64_t same = same_expert(ev[s]);
+        if (ev[s] >= 0 && (same & lanes_below) == 0) atomicAdd(&counts[ev[s]], __popcll(same));
+      }
+    }
+  }
+  __syncthreads();
+
+  // padded exclusive prefix (E <= 1024: one expert per thread)
+  const int pad = tid < E ? (counts[tid] + bs - 1) / bs * bs : 0;
+  int incl = pad;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) wave_sum[wave] = incl;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 16; ++w) incl += w < wave ? wave_sum[w] : 0;
+  const int start = incl - pad;
+  if (tid < E) cursor[tid] = start;
+  if (tid == E - 1) cursor[E] = incl;
+  __syncthreads();
+  const int total = cursor[E];
+  if (tid == 0) post_pad[0] = total;
+
+  // expert_ids
+  if (tid < E) {
+    for (int b = start / bs; b < incl / bs; ++b)
+      if (b < expert_ids_numel) expert_ids[b] = tid;
+  }
+  for (int64_t b = total / bs + tid; b < expert_ids_numel; b += 1024) expert_ids[b] = -1;
+
+  if (one_round) {
+    place_round(0);
+    return;
+  }
+  for (int64_t base = 0; base < numel; base += kRound) {
+    rank_round(base);
+    place_round(base);
+    __syncthreads();
+    for (int x = tid; x < E; x += 1024) cursor[x] += round_n[x];
     __syncthreads();
   }
 }
@@ -176,7 +257,7 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(
 hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, int bs, int* sorted,
                             int64_t sorted_numel, int* expert_ids, int64_t expert_ids_numel,
                             int* post_pad, const int* expert_map, hipStream_t stream) {
-  const size_t smem = (size_t)(2 * E + 1) * sizeof(int) + (size_t)16 * E;
+  const size_t smem = (size_t)(3 * E + 1) * sizeof(int) + (size_t)16 * E * sizeof(uint16_t);
   if (is64)
     hipLaunchKernelGGL((moe_align_kernel<int64_t>), dim3(1), dim3(1024), smem, stream,
                        reinterpret_cast<const int64_t*>(topk), numel, E, bs, sorted, sorted_numel,

@@ -37,7 +37,7 @@ def test_moe_align_kat():
 
 @pytest.mark.parametrize("tokens,E,topk,bs", [(16, 256, 8, 64), (2048, 256, 8, 64), (7, 8, 2, 16),
                                                (300, 64, 6, 8), (1000, 128, 4, 48),
-                                               (3000, 512, 8, 32)])
+                                               (3000, 512, 8, 32), (5000, 1024, 8, 16)])
 @pytest.mark.parametrize("id_dtype", [torch.int32, torch.int64])
 def test_moe_align_matches_oracle(tokens, E, topk, bs, id_dtype):
     gen = torch.Generator().manual_seed(tokens + E)
