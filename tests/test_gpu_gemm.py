@@ -1,6 +1,7 @@
 """GPU parity of marlin_gemm against the oracle (dequantize, fp32 matmul):
 max|out - ref| <= 1e-2 * max|ref| for every format, both dtypes, small and large M (the
-selector's 16/32/64/128-row tiles), split-K and K tails, bias, and the strided-A path."""
+selector's 16/32/64/128-row tiles), split-K and K tails, bias, the strided-A path, and the
+BASELINE configurations at full size."""
 import pytest
 import torch
 
@@ -112,3 +113,31 @@ def test_gemm_m_zero():
     a = torch.empty((0, k), dtype=torch.float16, device="cuda")
     out = _run(case, a)
     assert out.shape == (0, n)
+
+
+# BASELINE shapes at full size (the selector's production paths: the headline decode kernel
+# with its whole-group / K-split block mix, the multistage and 128-row kernels); rows of
+# large-M outputs are checked on a fixed sample spread over M.
+BASELINE_SHAPES = [
+    ("cfg1", "u4b8", torch.float16, 16, 4096, 4096),
+    ("cfg2", "u4", torch.bfloat16, 1, 5120, 34816),
+    ("cfg2", "u4", torch.bfloat16, 16, 5120, 34816),
+    ("cfg2", "u4", torch.bfloat16, 128, 5120, 34816),
+    ("cfg2", "u4", torch.bfloat16, 1024, 5120, 34816),
+    ("cfg3", "u8b128", torch.float16, 4096, 8192, 8192),
+    ("cfg4", "mxfp4", torch.bfloat16, 1, 3072, 12288),
+    ("cfg4", "mxfp4", torch.bfloat16, 512, 3072, 12288),
+    ("cfg4", "nvfp4", torch.bfloat16, 1, 3072, 12288),
+    ("cfg4", "nvfp4", torch.bfloat16, 64, 3072, 12288),
+]
+
+
+@pytest.mark.parametrize("name,fmt,dtype,m,k,n", BASELINE_SHAPES)
+def test_gemm_baseline_shapes(name, fmt, dtype, m, k, n):
+    print(f"case {name} fmt={fmt} m={m} k={k} n={n}", flush=True)
+    case = make_case(fmt, k, n, dtype, seed=m + k)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(m)).to(dtype)
+    out = _run(case, a.cuda()).cpu()
+    rows = torch.arange(m) if m <= 64 else torch.unique(torch.linspace(0, m - 1, 64).long())
+    ref = O.gemm_ref(a[rows], case.deq)
+    assert O.max_abs_rel_err(out[rows], ref) <= TOL
