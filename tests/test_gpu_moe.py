@@ -1,6 +1,7 @@
 """GPU parity of the MoE path: moe_align_block_size bit-exact against the stable-order
 oracle (plus the KAT from the reference tests), each moe_wna16_marlin_gemm stage against
-the oracle within 1e-2*max|ref|, and the full fused_marlin_moe layer."""
+the oracle within 1e-2*max|ref|, and the full fused_marlin_moe layer (small shapes against
+the oracle, the cfg5 shape at full size against the library's own dequantized experts)."""
 import numpy as np
 import pytest
 import torch
@@ -148,3 +149,45 @@ def test_silu_and_mul(dtype, rows, d):
     assert O.max_abs_rel_err(got, ref) <= 1e-2
     exact = (got.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
     assert exact >= 0.99, exact
+
+
+@pytest.mark.parametrize("T", [16, 2048])
+def test_fused_marlin_moe_baseline_shape(T):
+    """cfg5 at full size (E=256, top-8, H=3072, I=1536, uint4 + float zp g128, bf16): the
+    few-routes kernel (T=16) and the multistage MoE blocks (T=2048) against an fp32 layer
+    built from the library's dequantized experts (the dequantize op is bit-exact against the
+    oracle in test_gpu_repack_dequant.py), on 24 tokens spread over the batch."""
+    import bench
+    from marlin_v100_amd.fused_marlin_moe import fused_marlin_moe
+    from marlin_v100_amd.scalar_type import scalar_types
+
+    E, topk, H, I = 256, 8, 3072, 1536
+    dt = torch.bfloat16
+    print(f"case cfg5 T={T}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(T)
+    w13 = [bench.make_weights("u4", H, 2 * I, dt, gen) for _ in range(E)]
+    w2 = [bench.make_weights("u4", I, H, dt, gen) for _ in range(E)]
+    q13 = torch.stack([w["qweight"] for w in w13]); s13 = torch.stack([w["scales"] for w in w13])
+    z13 = torch.stack([w["zeros"] for w in w13])
+    q2 = torch.stack([w["qweight"] for w in w2]); s2 = torch.stack([w["scales"] for w in w2])
+    z2 = torch.stack([w["zeros"] for w in w2])
+    x = torch.randn((T, H), generator=gen, device="cuda").to(dt)
+    tw, ids = torch.topk(torch.softmax(torch.randn((T, E), generator=gen, device="cuda"), -1),
+                         topk, -1)
+    tw = (tw / tw.sum(-1, keepdim=True)).float().contiguous()
+    ids = ids.to(torch.int32).contiguous()
+    qid = scalar_types.uint4.id
+    out = fused_marlin_moe(x, q13, q2, None, None, s13, s2, tw, ids, qid, w1_zeros=z13,
+                           w2_zeros=z2, is_w1_zp_float=True, is_w2_zp_float=True)
+    tokens = torch.unique(torch.linspace(0, T - 1, 24).long()).tolist()
+    ref = torch.zeros((len(tokens), H), device="cuda")
+    for j, t in enumerate(tokens):
+        xt = x[t].float()[None]
+        for r in range(topk):
+            e = int(ids[t, r])
+            d13 = capi.dequantize(q13[e], s13[e], qid, H, 2 * I, dt, b_zeros=z13[e]).float()
+            h = xt @ d13
+            act = torch.nn.functional.silu(h[:, :I]) * h[:, I:]
+            d2 = capi.dequantize(q2[e], s2[e], qid, I, H, dt, b_zeros=z2[e]).float()
+            ref[j] += float(tw[t, r]) * (act @ d2)[0]
+    assert O.max_abs_rel_err(out[tokens].float().cpu(), ref.cpu()) <= 2 * TOL
