@@ -270,23 +270,85 @@ hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, i
 }
 
 // ---------------------------------------------------------------------------------------
-// moe_sum: out[t, h] = sum_k in[t, k, h], fp32 accumulation, one rounding.
+// moe_sum: out[t, h] = sum_k in[t, k, h] as the reference computes it
+// (moe_align_sum_kernels.cu:350-363, 597-639): for top-k 2..4 its kernel adds in the element
+// type, rounding after every addition; otherwise at::sum_out accumulates in fp32 and rounds
+// once.  `step_round` selects the former.
 // ---------------------------------------------------------------------------------------
+template <class AT>
+__device__ __forceinline__ float moe_sum_add(float s, float x, bool step_round) {
+  const float v = s + x;
+  return step_round ? raw16_to_float(to_raw16(v, AT{}), AT{}) : v;
+}
+
 template <class AT>
 __global__ void moe_sum_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
                                int64_t tokens, int topk, int64_t hidden) {
   const int64_t t = blockIdx.y;
+  const bool step_round = topk >= 2 && topk <= 4;
   for (int64_t h = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; h < hidden;
        h += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.f;
-    for (int k = 0; k < topk; ++k) s += raw16_to_float(in[(t * topk + k) * hidden + h], AT{});
+    for (int k = 0; k < topk; ++k)
+      s = moe_sum_add<AT>(s, raw16_to_float(in[(t * topk + k) * hidden + h], AT{}), step_round);
     out[t * hidden + h] = to_raw16(s, AT{});
+  }
+}
+
+// hidden % 8 == 0 and 16-byte aligned rows: 8 outputs per thread, each top-k slice read
+// with one 16-byte load, four slices in flight; same arithmetic as above.
+template <class AT>
+__global__ void moe_sum_kernel_v8(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
+                                  int64_t tokens, int topk, int64_t hidden) {
+  const int64_t per_row = hidden >> 3;
+  const int64_t n = tokens * per_row;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_row;
+    const int64_t h = (i - t * per_row) << 3;
+    const uint16_t* src = in + t * topk * hidden + h;
+    const bool step_round = topk >= 2 && topk <= 4;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < topk; k0 += 4) {
+      u32x4_t v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (k0 + j < topk) v[j] = *reinterpret_cast<const u32x4_t*>(src + (int64_t)(k0 + j) * hidden);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (k0 + j < topk) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            s[2 * w] = moe_sum_add<AT>(s[2 * w], raw16_to_float(v[j][w] & 0xffffu, AT{}), step_round);
+            s[2 * w + 1] = moe_sum_add<AT>(s[2 * w + 1], raw16_to_float(v[j][w] >> 16, AT{}), step_round);
+          }
+        }
+      }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = pack2(s[2 * w], s[2 * w + 1], AT{});
+    *reinterpret_cast<u32x4_t*>(out + t * hidden + h) = o;
   }
 }
 
 hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, int64_t hidden,
                           void* out, hipStream_t stream) {
   if (tokens == 0 || hidden == 0) return hipSuccess;
+  const uint16_t* i16v = reinterpret_cast<const uint16_t*>(in);
+  uint16_t* o16v = reinterpret_cast<uint16_t*>(out);
+  if (hidden % 8 == 0 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    const int64_t n = tokens * (hidden / 8);
+    const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 256 * 16);
+    if (bf16)
+      hipLaunchKernelGGL((moe_sum_kernel_v8<BF16>), dim3(blocks), dim3(256), 0, stream, i16v,
+                         o16v, tokens, topk, hidden);
+    else
+      hipLaunchKernelGGL((moe_sum_kernel_v8<F16>), dim3(blocks), dim3(256), 0, stream, i16v,
+                         o16v, tokens, topk, hidden);
+    return hipGetLastError();
+  }
   unsigned gx = (unsigned)((hidden + 255) / 256);
   if (gx > 64) gx = 64;
   dim3 grid(gx, (unsigned)tokens);

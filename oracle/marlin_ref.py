@@ -316,6 +316,21 @@ def gemm_ref(a: torch.Tensor, w_deq: torch.Tensor, bias: torch.Tensor | None = N
     return out
 
 
+def moe_sum(x: torch.Tensor) -> torch.Tensor:
+    """out[t, h] = sum_k x[t, k, h] for x [T, topk, H] in fp16/bf16, as the reference computes
+    it (csrc/moe/moe_align_sum_kernels.cu:350-363, 597-639): top-k 2..4 run its kernel, which
+    adds in the element type (one rounding per addition, k in order); every other top-k
+    falls through to at::sum_out (fp32 accumulation in k order, one rounding)."""
+    topk = x.shape[1]
+    step = 2 <= topk <= 4
+    s = torch.zeros(x[:, 0].shape, dtype=torch.float32)
+    for k in range(topk):
+        s = s + x[:, k].float()
+        if step:
+            s = s.to(x.dtype).float()
+    return s.to(x.dtype)
+
+
 # ---------------------------------------------------------------------------------------
 # moe_align_block_size (tests/test_marlin_moe.py:194-213 order; tail rules from
 # csrc/moe/moe_align_sum_kernels.cu:101-108, 126-133, 168-180)

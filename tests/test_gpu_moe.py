@@ -191,3 +191,23 @@ def test_fused_marlin_moe_baseline_shape(T):
             d2 = capi.dequantize(q2[e], s2[e], qid, I, H, dt, b_zeros=z2[e]).float()
             ref[j] += float(tw[t, r]) * (act @ d2)[0]
     assert O.max_abs_rel_err(out[tokens].float().cpu(), ref.cpu()) <= 2 * TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("topk", [1, 2, 3, 4, 6, 8])
+@pytest.mark.parametrize("tokens,hidden", [(33, 3072), (5, 100), (1, 8), (0, 64)])
+def test_moe_sum(dtype, topk, tokens, hidden):
+    """Native moe_sum bit-exact against the reference's arithmetic (per-addition rounding
+    for top-k 2..4, one fp32 rounding otherwise); hidden 3072 and 8 take the 16-byte path,
+    100 the element path."""
+    gen = torch.Generator().manual_seed(tokens * 7 + topk)
+    x = (torch.randn((tokens, topk, hidden), generator=gen) * 4).to(dtype)
+    out = torch.empty((tokens, hidden), dtype=dtype, device="cuda")
+    capi.moe_sum(x.cuda(), out)
+    assert torch.equal(out.cpu(), O.moe_sum(x))
+    if topk == 3 and dtype == torch.bfloat16 and tokens > 0:
+        kat = torch.zeros((1, 3, hidden), dtype=dtype)
+        kat[0, 0], kat[0, 1], kat[0, 2] = 1.0, 2.0 ** -8, 2.0 ** -8
+        o = torch.empty((1, hidden), dtype=dtype, device="cuda")
+        capi.moe_sum(kat.cuda(), o)
+        assert (o.cpu() == 1.0).all()

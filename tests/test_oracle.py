@@ -296,3 +296,19 @@ def test_planted_align_order_is_caught():
     reversed_within_expert = list(s[: n[0]])
     reversed_within_expert[0], reversed_within_expert[1] = reversed_within_expert[1], reversed_within_expert[0]
     assert reversed_within_expert != g["sorted_ids"]
+
+
+def test_moe_sum_rounding_modes():
+    # top-k 3: the reference kernel rounds after each addition in the element type
+    # (moe_align_sum_kernels.cu:350-363): 1 + 2^-8 ties to 1 in bf16, twice, so the result
+    # stays 1; one rounding of the fp32 sum gives 1 + 2^-7.  Top-k 8 (at::sum_out) rounds once.
+    x3 = torch.tensor([[[1.0], [2.0 ** -8], [2.0 ** -8]]], dtype=torch.bfloat16)
+    assert O.moe_sum(x3).item() == 1.0
+    x8 = torch.cat([x3, torch.zeros((1, 5, 1), dtype=torch.bfloat16)], dim=1)
+    assert O.moe_sum(x8).item() == 1.0 + 2.0 ** -7
+    # top-k 2: both rules agree (the pairwise sum is exact in fp32, then one rounding)
+    gen = torch.Generator().manual_seed(3)
+    x2 = torch.randn((64, 2, 32), generator=gen).to(torch.bfloat16)
+    assert torch.equal(O.moe_sum(x2), (x2[:, 0].float() + x2[:, 1].float()).to(torch.bfloat16))
+    # top-k 1: a copy
+    assert torch.equal(O.moe_sum(x2[:, :1]), x2[:, 0])
