@@ -169,31 +169,32 @@ void marlin_stream_kernel(const GemmParams p) {
   u32x4_t rb[D][NT][NL];
   MetaRaw rm[D][NT][RAWB];
 
-  auto load = [&](int s, auto dc) __attribute__((always_inline)) {
+  // Issue the loads of step s into ring slot dc: part q (0..3) takes the activation loads,
+  // weight tiles and metadata whose index is q mod 4; part -1 takes all of them.
+  auto load_part = [&](int s, auto dc, int q) __attribute__((always_inline)) {
     constexpr int d = decltype(dc)::value;
     const int k0 = s * 128;
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) ra[d][i] = *reinterpret_cast<const u32x4_t*>(a_src[i] + k0);
+    for (int i = 0; i < FPW; ++i)
+      if (q < 0 || i % 4 == q) ra[d][i] = *reinterpret_cast<const u32x4_t*>(a_src[i] + k0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
+      if (q >= 0 && t % 4 != q) continue;
       const uint32_t* tp = bptr + t * 256 + (int64_t)s * NL * chunk_stride;
 #pragma unroll
       for (int c = 0; c < NL; ++c)
         rb[d][t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(tp + c * chunk_stride));
-    }
-    if constexpr (GSM == GSM_BIG) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
+      if constexpr (GSM == GSM_BIG) {
         rm[d][t][0] = load_meta_raw<FMT, AT>(p, meta_base, k0 >> p.group_shift, (tn0 + t) * 16 + ln);
-    } else if constexpr (GSM == GSM_SMALL) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
+      } else if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
         for (int b = 0; b < 4; ++b)
           rm[d][t][b] = load_meta_raw<FMT, AT>(p, meta_base, (k0 + 32 * b + 8 * lg) >> p.group_shift,
                                                (tn0 + t) * 16 + ln);
+      }
     }
   };
+  auto load = [&](int s, auto dc) __attribute__((always_inline)) { load_part(s, dc, -1); };
 
   // Write this wave's fragments of ring slot dc into LDS buffer dc.
   auto stage = [&](auto dc) __attribute__((always_inline)) {
@@ -215,8 +216,12 @@ void marlin_stream_kernel(const GemmParams p) {
   };
 
   // Multiply one step: activations from LDS buffer lb, weights / metadata from registers.
+  // between(b) runs before k32 block b: the main loop issues a quarter of the next step's
+  // loads there, so the memory pipeline takes them while the previous block's MFMAs run
+  // (issued together right after the barrier, the four waves' loads queue for ~900 cycles)
   auto compute_core = [&](const Buf& lb, const u32x4_t (&bv)[NT][NL],
-                          const MetaRaw (&mv)[NT][RAWB], int nblocks) __attribute__((always_inline)) {
+                          const MetaRaw (&mv)[NT][RAWB], int nblocks,
+                          auto&& between) __attribute__((always_inline)) {
     if constexpr (M32) {
       // 32-row A operands straight from the 16x16 fragments (rows 32I + l%32, k-slice
       // 2h + l/32 of block b); B operands re-dealt from tile pairs with deal32().
@@ -230,6 +235,7 @@ void marlin_stream_kernel(const GemmParams p) {
       }
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
+        between(b);
         if (b < nblocks) {
           u32x4_t a32[MT32][2];
 #pragma unroll
@@ -270,6 +276,7 @@ void marlin_stream_kernel(const GemmParams p) {
       const u32x4_t ones = u32x4_t{IO::kOnes, IO::kOnes, IO::kOnes, IO::kOnes};
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
+        between(b);
         if (b < nblocks) {
           u32x4_t af[MT];
 #pragma unroll
@@ -320,6 +327,7 @@ void marlin_stream_kernel(const GemmParams p) {
       }
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
+        between(b);
         if (b < nblocks) {
           if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
@@ -357,9 +365,19 @@ void marlin_stream_kernel(const GemmParams p) {
     int s = s_begin;
     auto trip = [&](auto dc) __attribute__((always_inline)) {
       constexpr int d = decltype(dc)::value;
-      load(min(s + d + 2, last), std::integral_constant<int, (d + 2) % D>{});
+      // 16x16 form: the next step's loads go out a quarter per k32 block, between the
+      // blocks' MFMAs (cfg2 M=128: 101 -> 94 us; MoE stage 1 at T=2048: 706 -> 667 us).  The
+      // 128-row 32x32 form issues them up front (spread: 418 -> 436 us at M=1024).
+      constexpr bool kSpread = !M32;
+      if constexpr (!kSpread) load(min(s + d + 2, last), std::integral_constant<int, (d + 2) % D>{});
       stage(std::integral_constant<int, (d + 1) % D>{});
-      compute_core(buf(dc), rb[d], rm[d], 4);
+      compute_core(buf(dc), rb[d], rm[d], 4, [&](int q) __attribute__((always_inline)) {
+        if constexpr (kSpread) {
+          __builtin_amdgcn_sched_barrier(0);
+          load_part(min(s + d + 2, last), std::integral_constant<int, (d + 2) % D>{}, q);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      });
       __syncthreads();
     };
     for (int i = 0; i < full_trips; ++i, s += D) static_for<D>(trip);
@@ -367,9 +385,9 @@ void marlin_stream_kernel(const GemmParams p) {
     // remaining steps: s, s+1 (slots 0, 1); their loads and staging were issued above
     if (rem > 0) {
       stage(std::integral_constant<int, 1>{});
-      compute_core(lds_a0, rb[0], rm[0], 4);
+      compute_core(lds_a0, rb[0], rm[0], 4, [](int) {});
       __syncthreads();
-      if (rem > 1) compute_core(lds_a1, rb[1], rm[1], 4);
+      if (rem > 1) compute_core(lds_a1, rb[1], rm[1], 4, [](int) {});
     }
   }
 
@@ -414,7 +432,7 @@ void marlin_stream_kernel(const GemmParams p) {
       }
     }
     __syncthreads();
-    compute_core(lds_a2, bw, raw, nblocks);
+    compute_core(lds_a2, bw, raw, nblocks, [](int) {});
   }
 
   if constexpr (INT_B && GSM == GSM_CHANNEL && M32) {
