@@ -7,9 +7,10 @@ copies rotate through >= 512 MiB so the 256 MB Infinity Cache cannot hold them.
 
 The same JSON line carries every other BASELINE configuration (`configs`): cfg1 u4b8 fp16,
 cfg2 at M in {1,16,128,1024}, cfg3 u8b128 M=4096 (MFMA bound), cfg4 MXFP4/NVFP4 at
-M in {1,64,512}, and the cfg5 MoE layer (align + 2 grouped GEMMs + activation + top-k sum)
-at T in {16, 2048}; plus `roofline` for the headline kernel and `cpu_baseline` (the
-reference's CPU path: dequantize then fp32 matmul, timed on the host cores).
+M in {1,64,512}, the cfg5 MoE layer (align + 2 grouped GEMMs + activation + top-k sum)
+at T in {16, 2048} and its router (topk_softmax, top-8 of 256); plus `roofline` for the
+headline kernel and `cpu_baseline` (the reference's CPU path: dequantize then fp32 matmul,
+timed on the host cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
@@ -249,6 +250,45 @@ def moe_case(key, tokens, steps, warmup, seed):
             "vs_roofline": round(t / roof, 3)}
 
 
+def router_case(key, tokens, steps, warmup, seed):
+    """cfg5 router: topk_softmax over fp32 logits [T, 256], top-8, renormalized."""
+    import torch
+
+    from marlin_v100_amd import _custom_ops as ops
+
+    E, topk = 256, 8
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    logits = torch.randn((tokens, E), generator=gen, device="cuda")
+    w = torch.empty((tokens, topk), dtype=torch.float32, device="cuda")
+    ids = torch.empty((tokens, topk), dtype=torch.int32, device="cuda")
+    tei = torch.empty((tokens, topk), dtype=torch.int32, device="cuda")
+
+    def fn():
+        ops.topk_softmax(w, ids, tei, logits, True, None)
+
+    # eager calls are bound by host dispatch (torch op -> C ABI -> launch); the device rate
+    # comes from a captured graph of 50 back-to-back calls (the kernel writes no memset node)
+    t_eager = time_calls([fn], steps, warmup)
+    per_graph = 50
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(per_graph):
+                fn()
+    torch.cuda.current_stream().wait_stream(side)
+    replays = max(2, steps // per_graph)
+    t = time_calls([graph.replay], replays, 2) / per_graph
+    alg_bytes = tokens * E * 4 + tokens * topk * 12
+    return {"key": key, "T": tokens, "E": E, "topk": topk, "us": round(t * 1e6, 2),
+            "us_eager_dispatch": round(t_eager * 1e6, 2), "alg_bytes": alg_bytes,
+            "alg_GBs": round(alg_bytes / t / 1e9, 1),
+            "hbm_frac": round(alg_bytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 # ---------------------------------------------------------------------------------------
 # CPU reference path (bounded sample), timed on the host cores
 # ---------------------------------------------------------------------------------------
@@ -334,6 +374,11 @@ def main() -> int:
                 continue
             configs[key] = moe_case(key, t, max(10, args.steps // 10), max(3, args.warmup // 4), 1005)
             print(f"# {key}: {configs[key]['layer_us']} us", file=sys.stderr, flush=True)
+        for key, t in (("cfg5_router_t16", 16), ("cfg5_router_t2048", 2048)):
+            if only and key not in only:
+                continue
+            configs[key] = router_case(key, t, args.steps, args.warmup, 1005)
+            print(f"# {key}: {configs[key]['us']} us", file=sys.stderr, flush=True)
 
     t = head["us"] / 1e6
     # HBM traffic per launch of the headline kernel, from the rocprofv3 FETCH_SIZE /

@@ -45,6 +45,7 @@ typedef enum {
   MARLIN_DTYPE_INT64 = 6,
   MARLIN_DTYPE_UINT8 = 7,
   MARLIN_DTYPE_INT8 = 8,
+  MARLIN_DTYPE_UINT32 = 9,
 } marlin_dtype_t;
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -200,6 +201,39 @@ marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t 
  */
 marlin_status_t marlin_silu_and_mul(const void* input, marlin_dtype_t dtype, int64_t rows,
                                     int64_t d, void* out, marlin_stream_t stream);
+
+/*
+ * MoE router, softmax scoring.  gating_output: [num_tokens, num_experts] fp16, bf16 or fp32,
+ * contiguous.  Per row: scores = softmax(row) in fp32; the top_k experts by score + bias[e]
+ * (bias optional, fp32 [num_experts]) in descending order, ties to the lower expert index;
+ * topk_weights [num_tokens, top_k] fp32 = the unbiased scores, divided by their sum when
+ * renormalize != 0 (a zero sum divides by 1); topk_indices [num_tokens, top_k] in int32,
+ * uint32 or int64; token_expert_indices [num_tokens, top_k] int32 = j * num_tokens + t.
+ * This build supports num_experts <= 4096 and top_k <= 256 (MARLIN_STATUS_NOT_SUPPORTED
+ * beyond).
+ * Replaces torch.ops._moe_C.topk_softmax (reference csrc/moe/topk_softmax_kernels.cu:773-809,
+ * argument checks :732-739; schema csrc/moe/torch_bindings_marlin.cpp:5-9).
+ */
+marlin_status_t marlin_topk_softmax(float* topk_weights, void* topk_indices,
+                                    marlin_dtype_t topk_indices_dtype,
+                                    int32_t* token_expert_indices, int64_t top_k,
+                                    const void* gating_output, marlin_dtype_t gating_dtype,
+                                    int64_t num_tokens, int64_t num_experts, int renormalize,
+                                    const float* bias, int64_t bias_numel,
+                                    marlin_stream_t stream);
+
+/*
+ * MoE router, sigmoid scoring: as marlin_topk_softmax with scores = 1 / (1 + exp(-x)).
+ * Replaces torch.ops._moe_C.topk_sigmoid (reference csrc/moe/topk_softmax_kernels.cu:811-847;
+ * schema csrc/moe/torch_bindings_marlin.cpp:11-15).
+ */
+marlin_status_t marlin_topk_sigmoid(float* topk_weights, void* topk_indices,
+                                    marlin_dtype_t topk_indices_dtype,
+                                    int32_t* token_expert_indices, int64_t top_k,
+                                    const void* gating_output, marlin_dtype_t gating_dtype,
+                                    int64_t num_tokens, int64_t num_experts, int renormalize,
+                                    const float* bias, int64_t bias_numel,
+                                    marlin_stream_t stream);
 
 #ifdef __cplusplus
 }

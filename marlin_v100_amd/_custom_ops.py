@@ -1,5 +1,5 @@
 """Python op wrappers with the reference's names and signatures
-(reference vllm/_custom_ops.py:1163-1351, 2129-2168, 2361-2483).
+(reference vllm/_custom_ops.py:1163-1351, 2129-2168, 2286-2318, 2361-2483).
 
 Each wrapper forwards to the torch op registered by _C.so / _moe_C.so, which validates the
 arguments and calls the C ABI of libmarlin_mi355x.so.  Fake (meta) implementations let
@@ -99,6 +99,22 @@ def _marlin_gemm_fake(a, c, b_q_weight, b_bias, b_scales, a_scales, global_scale
 
 
 # ---- MoE ---------------------------------------------------------------------------------
+
+def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                 token_expert_indices: torch.Tensor, gating_output: torch.Tensor,
+                 renormalize: bool = False,
+                 e_score_correction_bias: torch.Tensor | None = None) -> None:
+    torch.ops._moe_C.topk_softmax(topk_weights, topk_ids, token_expert_indices, gating_output,
+                                  renormalize, e_score_correction_bias)
+
+
+def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                 token_expert_indices: torch.Tensor, gating_output: torch.Tensor,
+                 renormalize: bool = False,
+                 e_score_correction_bias: torch.Tensor | None = None) -> None:
+    torch.ops._moe_C.topk_sigmoid(topk_weights, topk_ids, token_expert_indices, gating_output,
+                                  renormalize, e_score_correction_bias)
+
 
 def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: int,
                          sorted_token_ids: torch.Tensor, experts_ids: torch.Tensor,

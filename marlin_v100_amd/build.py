@@ -39,6 +39,7 @@ HIP_SOURCES = [
     "capi.hip",
     "repack.hip",
     "aux_kernels.hip",
+    "router_kernels.hip",
     "gemm_u4b8.hip",
     "gemm_u4.hip",
     "gemm_u8b128.hip",

@@ -14,7 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmarlin_mi355x.so")
 
 # marlin_dtype_t
-F16, BF16, F32, F8E4M3, F8E8M0, I32, I64, U8, I8 = range(9)
+F16, BF16, F32, F8E4M3, F8E8M0, I32, I64, U8, I8, U32 = range(10)
 _DT = {
     torch.float16: F16,
     torch.bfloat16: BF16,
@@ -25,6 +25,7 @@ _DT = {
     torch.int64: I64,
     torch.uint8: U8,
     torch.int8: I8,
+    torch.uint32: U32,
 }
 
 STATUS_OK, STATUS_INVALID, STATUS_NOT_SUPPORTED, STATUS_HIP = range(4)
@@ -50,6 +51,8 @@ SIGNATURES = {
                                _I64, _I, _P, _P]),
     "marlin_moe_sum": (_I, [_P, _I, _I64, _I64, _I64, _P, _P]),
     "marlin_silu_and_mul": (_I, [_P, _I, _I64, _I64, _P, _P]),
+    "marlin_topk_softmax": (_I, [_P, _P, _I, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I64, _P]),
+    "marlin_topk_sigmoid": (_I, [_P, _P, _I, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I64, _P]),
 }
 
 _lib = None
@@ -183,3 +186,17 @@ def silu_and_mul(out, x):
     rows = x.numel() // max(2 * d, 1)
     _check(load().marlin_silu_and_mul(_ptr(x), _dt(x), rows, d, _ptr(out), _stream()))
     return out
+
+
+def topk_gating(gating, topk, renormalize=False, bias=None, scoring="softmax",
+                ids_dtype=torch.int32):
+    """Router top-k over gating [T, E]: returns (weights f32, ids, token_expert_indices)."""
+    t, e = gating.shape
+    dev = gating.device
+    w = torch.empty((t, topk), dtype=torch.float32, device=dev)
+    ids = torch.empty((t, topk), dtype=ids_dtype, device=dev)
+    tei = torch.empty((t, topk), dtype=torch.int32, device=dev)
+    fn = load().marlin_topk_softmax if scoring == "softmax" else load().marlin_topk_sigmoid
+    _check(fn(_ptr(w), _ptr(ids), _DT[ids_dtype], _ptr(tei), topk, _ptr(gating), _dt(gating), t,
+              e, int(renormalize), _ptr(bias), _numel(bias), _stream()))
+    return w, ids, tei

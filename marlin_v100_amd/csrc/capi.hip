@@ -906,3 +906,66 @@ marlin_status_t marlin_silu_and_mul(const void* input, marlin_dtype_t dtype, int
 }
 
 }  // extern "C"
+
+namespace {
+
+marlin_status_t topk_gating(bool sigmoid, float* topk_weights, void* topk_indices,
+                            marlin_dtype_t ids_dtype, int32_t* token_expert_indices,
+                            int64_t top_k, const void* gating, marlin_dtype_t gating_dtype,
+                            int64_t num_tokens, int64_t num_experts, int renormalize,
+                            const float* bias, int64_t bias_numel, marlin_stream_t stream) {
+  return guarded([&] {
+    check(gating_dtype == MARLIN_DTYPE_FLOAT32 || gating_dtype == MARLIN_DTYPE_FLOAT16 ||
+              gating_dtype == MARLIN_DTYPE_BFLOAT16,
+          "Unsupported gating_output data type: ", (int)gating_dtype);
+    check(ids_dtype == MARLIN_DTYPE_INT32 || ids_dtype == MARLIN_DTYPE_UINT32 ||
+              ids_dtype == MARLIN_DTYPE_INT64,
+          "topk_indices must be int32, uint32 or int64");
+    check(num_experts > 0, "num_experts must be positive");
+    check(num_tokens >= 0, "invalid num_tokens");
+    check(top_k >= 1 && top_k <= num_experts, "topk must be in [1, num_experts]");
+    if (bias) check(bias_numel == num_experts, "bias size mismatch, expected: ", num_experts);
+    check_supported(num_experts <= kRouterMaxExperts, "this build supports at most ",
+                    kRouterMaxExperts, " experts per router row");
+    check_supported(top_k <= kMaxK, "this build supports topk <= ", kMaxK);
+    if (num_tokens == 0) return;
+    check(topk_weights && topk_indices && token_expert_indices && gating, "null tensor pointer");
+    const int in_kind = gating_dtype == MARLIN_DTYPE_FLOAT16 ? 0
+                        : gating_dtype == MARLIN_DTYPE_BFLOAT16 ? 1 : 2;
+    const int ids_kind = ids_dtype == MARLIN_DTYPE_INT32 ? 0 : ids_dtype == MARLIN_DTYPE_UINT32 ? 1 : 2;
+    check_hip(launch_topk_gating(sigmoid, in_kind, gating, bias, topk_weights, topk_indices,
+                                 ids_kind, token_expert_indices, num_tokens, (int)num_experts,
+                                 (int)top_k, renormalize != 0, (hipStream_t)stream),
+              sigmoid ? "topk_sigmoid launch" : "topk_softmax launch");
+  });
+}
+
+}  // namespace
+
+extern "C" {
+
+marlin_status_t marlin_topk_softmax(float* topk_weights, void* topk_indices,
+                                    marlin_dtype_t topk_indices_dtype,
+                                    int32_t* token_expert_indices, int64_t top_k,
+                                    const void* gating_output, marlin_dtype_t gating_dtype,
+                                    int64_t num_tokens, int64_t num_experts, int renormalize,
+                                    const float* bias, int64_t bias_numel,
+                                    marlin_stream_t stream) {
+  return topk_gating(false, topk_weights, topk_indices, topk_indices_dtype, token_expert_indices,
+                     top_k, gating_output, gating_dtype, num_tokens, num_experts, renormalize,
+                     bias, bias_numel, stream);
+}
+
+marlin_status_t marlin_topk_sigmoid(float* topk_weights, void* topk_indices,
+                                    marlin_dtype_t topk_indices_dtype,
+                                    int32_t* token_expert_indices, int64_t top_k,
+                                    const void* gating_output, marlin_dtype_t gating_dtype,
+                                    int64_t num_tokens, int64_t num_experts, int renormalize,
+                                    const float* bias, int64_t bias_numel,
+                                    marlin_stream_t stream) {
+  return topk_gating(true, topk_weights, topk_indices, topk_indices_dtype, token_expert_indices,
+                     top_k, gating_output, gating_dtype, num_tokens, num_experts, renormalize,
+                     bias, bias_numel, stream);
+}
+
+}  // extern "C"

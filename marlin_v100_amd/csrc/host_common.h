@@ -24,6 +24,13 @@ hipError_t launch_silu_and_mul(const void* x, bool bf16, int64_t rows, int64_t d
                                hipStream_t stream);
 hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, int64_t hidden,
                           void* out, hipStream_t stream);
+// Router limits: experts per row held in one wavefront's registers, chosen experts per row.
+constexpr int kRouterMaxExperts = 64 * 64;
+constexpr int kMaxK = 256;
+// in_kind 0 fp16 / 1 bf16 / 2 fp32; ids_kind 0 int32 / 1 uint32 / 2 int64.
+hipError_t launch_topk_gating(bool sigmoid, int in_kind, const void* gating, const float* bias,
+                              float* weights, void* ids, int ids_kind, int* tei, int64_t T, int E,
+                              int k, bool renorm, hipStream_t stream);
 
 // One GEMM launch configuration.
 struct GemmLaunch {

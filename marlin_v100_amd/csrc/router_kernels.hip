@@ -1,0 +1,294 @@
+// router_kernels.hip -- MoE router: topk_softmax / topk_sigmoid.
+//
+// Semantics (reference csrc/moe/topk_softmax_kernels.cu): per token row, scores are the fp32
+// softmax over the experts (:75-133) or the elementwise sigmoid (:135-153); experts are chosen
+// by score + bias (bias optional, fp32 [E]) in descending order, ties going to the lower
+// expert index (:488, :508); the returned weight is the unbiased score (:223-225), divided by
+// the sum of the k chosen scores when renormalize is set (a zero sum divides by 1, :551-560);
+// token_expert_indices[t, j] = j * num_tokens + t (:226, :527).
+//
+// Layout on MI355X: one 64-lane wavefront per token.  Lane l holds experts l + 64*j for
+// j < VPL in registers, so each j is one coalesced 64-element load of the row; the softmax
+// max / sum and each of the k argmax steps are reductions across the wave in VALU
+// cross-lane operations (DPP, permlane swaps).  No LDS, no workspace: the reference's E > 256 / non-power-of-two path goes through a
+// [T, E] fp32 workspace (:774-777); here every E <= 64 * 64 stays in registers.
+#include <algorithm>
+
+#include "device_common.h"
+#include "host_common.h"
+
+namespace mmi {
+
+namespace {
+
+template <class IT>
+struct ScoreIn;
+template <>
+struct ScoreIn<float> {
+  using raw = float;
+  __device__ static float get(const float* p, int64_t i) { return p[i]; }
+};
+template <>
+struct ScoreIn<F16> {
+  using raw = uint16_t;
+  __device__ static float get(const uint16_t* p, int64_t i) { return raw16_to_float(p[i], F16{}); }
+};
+template <>
+struct ScoreIn<BF16> {
+  using raw = uint16_t;
+  __device__ static float get(const uint16_t* p, int64_t i) {
+    return raw16_to_float(p[i], BF16{});
+  }
+};
+
+// Cross-lane steps without LDS round trips: DPP inside each 16-lane row (row_ror:8,
+// row_ror:4, then quad xor 2 and xor 1), then v_permlane16_swap / v_permlane32_swap across
+// rows.  permlane{16,32}_swap(v, v) returns the lane's own row value and its partner row's
+// value (in row order), so combining the pair with a commutative operation gives every lane
+// the same result.  In this order every lane also forms the same association of partial
+// results, so a float sum is bit-identical on all 64 lanes.
+constexpr int kDppRor8 = 0x128;
+constexpr int kDppRor4 = 0x124;
+constexpr int kDppXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kDppXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+// The two values of a row pair (16-lane rows 2r, 2r+1) or half pair (lanes 0-31, 32-63).
+struct Pair {
+  float v0, v1;
+  int i0, i1;
+};
+__device__ __forceinline__ Pair swap16(float v, int i) {
+  const auto sv = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v),
+                                                   __builtin_bit_cast(int, v), false, false);
+  const auto si = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+  return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1]),
+          (int)si[0], (int)si[1]};
+}
+__device__ __forceinline__ Pair swap32(float v, int i) {
+  const auto sv = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v),
+                                                   __builtin_bit_cast(int, v), false, false);
+  const auto si = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+  return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1]),
+          (int)si[0], (int)si[1]};
+}
+
+// (value, index) order: the larger value wins, equal values go to the lower index.
+__device__ __forceinline__ void take_better(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+  take_better(v, i, dpp<CTRL>(v), dpp<CTRL>(i));
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  argmax_dpp<kDppRor8>(v, i);
+  argmax_dpp<kDppRor4>(v, i);
+  argmax_dpp<kDppXor2>(v, i);
+  argmax_dpp<kDppXor1>(v, i);
+  Pair p = swap16(v, i);
+  v = p.v0;
+  i = p.i0;
+  take_better(v, i, p.v1, p.i1);
+  p = swap32(v, i);
+  v = p.v0;
+  i = p.i0;
+  take_better(v, i, p.v1, p.i1);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppRor8>(v));
+  v = fmaxf(v, dpp<kDppRor4>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  Pair p = swap16(v, 0);
+  v = fmaxf(p.v0, p.v1);
+  p = swap32(v, 0);
+  return fmaxf(p.v0, p.v1);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + dpp<kDppRor8>(v);
+  v = v + dpp<kDppRor4>(v);
+  v = v + dpp<kDppXor2>(v);
+  v = v + dpp<kDppXor1>(v);
+  Pair p = swap16(v, 0);
+  v = p.v0 + p.v1;
+  p = swap32(v, 0);
+  return p.v0 + p.v1;
+}
+
+constexpr int kSoftmax = 0;
+constexpr int kSigmoid = 1;
+constexpr int kWavesPerBlock = 4;
+
+// VPL: experts per lane (E <= 64 * VPL).  OT: id output type (int32_t, uint32_t, int64_t).
+template <class IT, int VPL, int SF, class OT>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void topk_gating_kernel(
+    const typename ScoreIn<IT>::raw* __restrict__ gating, const float* __restrict__ bias,
+    float* __restrict__ weights, OT* __restrict__ ids, int* __restrict__ token_expert_indices,
+    int64_t num_tokens, int num_experts, int k, int renormalize) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (t >= num_tokens) return;  // whole wave leaves together; no barriers below
+  const typename ScoreIn<IT>::raw* row = gating + t * num_experts;
+
+  float score[VPL];
+  float choice[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    score[j] = e < num_experts ? ScoreIn<IT>::get(row, e) : -INFINITY;
+  }
+
+  if constexpr (SF == kSoftmax) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) m = fmaxf(m, score[j]);
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane + 64 * j;
+      score[j] = e < num_experts ? expf(score[j] - m) : 0.0f;
+      s += score[j];
+    }
+    const float inv = 1.0f / wave_sum(s);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) score[j] *= inv;
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) score[j] = 1.0f / (1.0f + expf(-score[j]));
+  }
+
+  uint64_t live = 0;  // bit j: expert lane + 64*j exists and is not chosen yet
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < num_experts) {
+      live |= 1ull << j;
+      choice[j] = bias ? score[j] + bias[e] : score[j];
+    } else {
+      choice[j] = -INFINITY;
+    }
+  }
+
+  float* wrow = weights + t * k;
+  OT* irow = ids + t * k;
+  int* srow = token_expert_indices + t * k;
+  float sum = 0.0f;
+  float kept[kMaxK / 64];  // lane l keeps the weight of round 64*s + l in kept[s]
+#pragma unroll
+  for (int s = 0; s < kMaxK / 64; ++s) kept[s] = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    // lane-local argmax over its live experts in ascending expert order; the first live
+    // slot is taken even when its choice is -inf, so such an expert still wins over an
+    // absent one
+    float bv = -INFINITY;
+    int bi = num_experts;
+    float bw = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (((live >> j) & 1) && (choice[j] > bv || bi == num_experts)) {
+        bv = choice[j];
+        bi = lane + 64 * j;
+        bw = score[j];
+      }
+    }
+    float wv = bv;
+    int wi = bi;
+    wave_argmax(wv, wi);
+    // the winner's unbiased score comes from the lane that owns it (wi is wave-uniform)
+    wi = __builtin_amdgcn_readfirstlane(wi);
+    const float w = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bw), wi & 63));
+    if ((wi & 63) == lane) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        if (j == (wi >> 6)) live &= ~(1ull << j);
+    }
+    sum += w;
+    if (lane == (r & 63)) {
+#pragma unroll
+      for (int s = 0; s < kMaxK / 64; ++s)
+        if (s == (r >> 6)) kept[s] = w;
+    }
+    if (lane == 0) {
+      irow[r] = (OT)wi;
+      srow[r] = (int)((int64_t)r * num_tokens + t);
+    }
+  }
+  const float denom = renormalize ? (sum > 0.0f ? sum : 1.0f) : 1.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxK / 64; ++s) {
+    const int r = 64 * s + lane;
+    if (r < k) wrow[r] = renormalize ? kept[s] / denom : kept[s];
+  }
+}
+
+template <class IT, int SF, class OT>
+hipError_t launch_vpl(const void* gating, const float* bias, float* w, OT* ids, int* tei,
+                      int64_t T, int E, int k, bool renorm, hipStream_t stream) {
+  const dim3 grid((unsigned)((T + kWavesPerBlock - 1) / kWavesPerBlock));
+  const dim3 block(64 * kWavesPerBlock);
+  using R = typename ScoreIn<IT>::raw;
+  const R* g = reinterpret_cast<const R*>(gating);
+#define MMI_ROUTER_LAUNCH(V)                                                                  \
+  hipLaunchKernelGGL((topk_gating_kernel<IT, V, SF, OT>), grid, block, 0, stream, g, bias, w, \
+                     ids, tei, T, E, k, (int)renorm)
+  const int vpl = (E + 63) / 64;
+  if (vpl <= 1) MMI_ROUTER_LAUNCH(1);
+  else if (vpl <= 2) MMI_ROUTER_LAUNCH(2);
+  else if (vpl <= 4) MMI_ROUTER_LAUNCH(4);
+  else if (vpl <= 8) MMI_ROUTER_LAUNCH(8);
+  else if (vpl <= 16) MMI_ROUTER_LAUNCH(16);
+  else if (vpl <= 32) MMI_ROUTER_LAUNCH(32);
+  else MMI_ROUTER_LAUNCH(64);
+#undef MMI_ROUTER_LAUNCH
+  return hipGetLastError();
+}
+
+template <int SF, class OT>
+hipError_t launch_in(int in_kind, const void* gating, const float* bias, float* w, OT* ids,
+                     int* tei, int64_t T, int E, int k, bool renorm, hipStream_t stream) {
+  switch (in_kind) {
+    case 0: return launch_vpl<F16, SF, OT>(gating, bias, w, ids, tei, T, E, k, renorm, stream);
+    case 1: return launch_vpl<BF16, SF, OT>(gating, bias, w, ids, tei, T, E, k, renorm, stream);
+    default: return launch_vpl<float, SF, OT>(gating, bias, w, ids, tei, T, E, k, renorm, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_topk_gating(bool sigmoid, int in_kind, const void* gating, const float* bias,
+                              float* weights, void* ids, int ids_kind, int* tei, int64_t T, int E,
+                              int k, bool renorm, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  if (ids_kind == 2) {
+    int64_t* o = reinterpret_cast<int64_t*>(ids);
+    return sigmoid ? launch_in<kSigmoid>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream)
+                   : launch_in<kSoftmax>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream);
+  }
+  if (ids_kind == 1) {
+    uint32_t* o = reinterpret_cast<uint32_t*>(ids);
+    return sigmoid ? launch_in<kSigmoid>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream)
+                   : launch_in<kSoftmax>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream);
+  }
+  int32_t* o = reinterpret_cast<int32_t*>(ids);
+  return sigmoid ? launch_in<kSigmoid>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream)
+                 : launch_in<kSoftmax>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream);
+}
+
+}  // namespace mmi

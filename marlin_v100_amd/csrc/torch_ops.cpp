@@ -3,8 +3,8 @@
 // Built twice: with MMI_EXT_NAME=_C it registers torch.ops._C.{marlin_gemm,
 // gptq_marlin_repack, awq_marlin_repack} (schemas byte-identical to the reference
 // csrc/torch_bindings_marlin.cpp:6-21); with MMI_EXT_NAME=_moe_C it registers
-// torch.ops._moe_C.{moe_align_block_size, moe_wna16_marlin_gemm, moe_sum}
-// (csrc/moe/torch_bindings_marlin.cpp:17-47).  The _C build also registers the inspection op
+// torch.ops._moe_C.{topk_softmax, topk_sigmoid, moe_align_block_size, moe_wna16_marlin_gemm,
+// moe_sum} (csrc/moe/torch_bindings_marlin.cpp:5-47).  The _C build also registers the inspection op
 // torch.ops._marlin_mi355x.dequantize.  Tensor-level checks (device, contiguity, ranks,
 // shapes) mirror the reference's TORCH_CHECKs; everything else is validated by the C ABI,
 // whose messages are rethrown unchanged.
@@ -35,6 +35,7 @@ marlin_dtype_t to_mdt(at::ScalarType t) {
     case at::kLong: return MARLIN_DTYPE_INT64;
     case at::kByte: return MARLIN_DTYPE_UINT8;
     case at::kChar: return MARLIN_DTYPE_INT8;
+    case at::kUInt32: return MARLIN_DTYPE_UINT32;
     default: return (marlin_dtype_t)-1;
   }
 }
@@ -393,7 +394,63 @@ void op_moe_sum(at::Tensor& input, at::Tensor& output) {
                          input.size(1), input.size(2), output.data_ptr(), cur_stream(input)));
 }
 
+// reference topk_softmax / topk_sigmoid (csrc/moe/topk_softmax_kernels.cu:773-847): outputs
+// are caller-allocated [tokens, topk]; topk = topk_weights.size(-1), experts =
+// gating_output.size(-1), tokens = gating_output.numel() / experts.
+template <bool Sigmoid>
+void op_topk_gating(at::Tensor& topk_weights, at::Tensor& topk_indices,
+                    at::Tensor& token_expert_indices, at::Tensor& gating_output, bool renormalize,
+                    std::optional<at::Tensor> bias) {
+  TORCH_CHECK(gating_output.is_cuda() && gating_output.is_contiguous(),
+              "gating_output must be a contiguous GPU tensor");
+  const int64_t num_experts = gating_output.size(-1);
+  TORCH_CHECK(num_experts > 0, "gating_output has no experts");
+  const int64_t num_tokens = gating_output.numel() / num_experts;
+  const int64_t topk = topk_weights.size(-1);
+  TORCH_CHECK(topk_weights.is_cuda() && topk_weights.is_contiguous() &&
+                  topk_weights.scalar_type() == at::kFloat,
+              "topk_weights must be a contiguous float32 GPU tensor");
+  TORCH_CHECK(topk_indices.is_cuda() && topk_indices.is_contiguous(),
+              "topk_indices must be a contiguous GPU tensor");
+  TORCH_CHECK(token_expert_indices.is_cuda() && token_expert_indices.is_contiguous() &&
+                  token_expert_indices.scalar_type() == at::kInt,
+              "token_expert_indices must be a contiguous int32 GPU tensor");
+  for (const at::Tensor* t : {&topk_weights, &topk_indices, &token_expert_indices}) {
+    TORCH_CHECK(t->numel() == num_tokens * topk, "router output shape mismatch: expected ",
+                num_tokens, " x ", topk, " elements");
+  }
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->scalar_type() == at::kFloat, "bias tensor must be float32");
+    TORCH_CHECK(bias->dim() == 1, "bias tensor must be 1D");
+    TORCH_CHECK(bias->size(0) == num_experts, "bias size mismatch, expected: ", num_experts);
+    TORCH_CHECK(bias->is_contiguous(), "bias tensor must be contiguous");
+    TORCH_CHECK(bias->is_cuda(), "bias tensor must be on the GPU");
+  }
+  TORCH_CHECK(to_mdt(topk_indices.scalar_type()) == MARLIN_DTYPE_INT32 ||
+                  to_mdt(topk_indices.scalar_type()) == MARLIN_DTYPE_UINT32 ||
+                  to_mdt(topk_indices.scalar_type()) == MARLIN_DTYPE_INT64,
+              "topk_indices must be int32, uint32 or int64");
+  const at::OptionalDeviceGuard guard(gating_output.device());
+  const auto fn = Sigmoid ? marlin_topk_sigmoid : marlin_topk_softmax;
+  rethrow(fn(topk_weights.data_ptr<float>(), topk_indices.data_ptr(),
+             to_mdt(topk_indices.scalar_type()), token_expert_indices.data_ptr<int32_t>(), topk,
+             gating_output.data_ptr(), to_mdt(gating_output.scalar_type()), num_tokens,
+             num_experts, renormalize ? 1 : 0,
+             bias.has_value() ? bias->data_ptr<float>() : nullptr,
+             bias.has_value() ? bias->numel() : 0, cur_stream(gating_output)));
+}
+
 TORCH_LIBRARY(_moe_C, m) {
+  m.def(
+      "topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! "
+      "token_expert_indices, Tensor gating_output, bool renormalize, Tensor? "
+      "bias) -> ()");
+  m.impl("topk_softmax", torch::kCUDA, &op_topk_gating<false>);
+  m.def(
+      "topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! "
+      "token_expert_indices, Tensor gating_output, bool renormalize, Tensor? "
+      "bias) -> ()");
+  m.impl("topk_sigmoid", torch::kCUDA, &op_topk_gating<true>);
   m.def(
       "moe_align_block_size(Tensor topk_ids, int num_experts,"
       "                     int block_size, Tensor! sorted_token_ids,"

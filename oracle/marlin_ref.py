@@ -400,6 +400,43 @@ def route_topk(logits: torch.Tensor, topk: int):
     return w.contiguous(), ids.to(torch.int32).contiguous()
 
 
+# ---------------------------------------------------------------------------------------
+# MoE router: topk_softmax / topk_sigmoid (reference test oracle tests/test_marlin_moe.py:111-133;
+# kernel rules csrc/moe/topk_softmax_kernels.cu: softmax :75-133, sigmoid :135-153, selection by
+# score + bias with ties to the lower expert index :446-460, :488, :508, unbiased output
+# weights :223-225, renormalization by the chosen sum with a zero sum dividing by 1 :551-560,
+# token_expert_indices = j * T + t :226, :527)
+# ---------------------------------------------------------------------------------------
+
+def topk_gating(gating: np.ndarray, topk: int, renormalize: bool = False,
+                bias: np.ndarray | None = None, scoring: str = "softmax"):
+    """gating [T, E] (any float dtype); returns (weights f32 [T, k], ids i32 [T, k],
+    token_expert_indices i32 [T, k]).  Scores are computed in float32."""
+    x = np.asarray(gating, dtype=np.float32)
+    t, e = x.shape
+    if scoring == "softmax":
+        ex = np.exp(x - x.max(axis=1, keepdims=True), dtype=np.float32)
+        scores = (ex / ex.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    elif scoring == "sigmoid":
+        scores = (np.float32(1.0) / (np.float32(1.0) + np.exp(-x, dtype=np.float32))).astype(
+            np.float32)
+    else:
+        raise ValueError(scoring)
+    choice = scores if bias is None else (scores + np.asarray(bias, np.float32)[None, :])
+    # descending choice, ties to the lower index: lexsort's last key is the primary one
+    cols = np.arange(e)
+    ids = np.empty((t, topk), dtype=np.int32)
+    for r in range(t):
+        order = np.lexsort((cols, -choice[r].astype(np.float64)))
+        ids[r] = order[:topk]
+    w = np.take_along_axis(scores, ids.astype(np.int64), axis=1).astype(np.float32)
+    if renormalize:
+        s = w.sum(axis=1, keepdims=True, dtype=np.float32)
+        w = (w / np.where(s > 0, s, np.float32(1.0))).astype(np.float32)
+    tei = (np.arange(topk, dtype=np.int64)[None, :] * t + np.arange(t)[:, None]).astype(np.int32)
+    return w, ids, tei
+
+
 def max_abs_rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:
     """max|out - ref| / max|ref| (the BASELINE tolerance metric)."""
     ref = ref.to(torch.float32)

@@ -5,9 +5,15 @@ imported or executed): the values below are copied from the cited test assertion
                          vllm/scalar_type.py:83-90 (ids as listed for the op ABI)
   moe_align_kat.json   : tests/test_marlin_moe.py:274-291 (_moe_align_block_size_reference)
   bias_perm.json       : csrc/quantization/marlin/sm70_marlin_bias.cuh:20-23
+  topk_softmax_kat.json: inputs of tests/test_marlin_moe.py:248-272 (fp16 gating, fp32 bias,
+                         top-2, renormalize); expected ids and weights evaluated here from the
+                         closed form in float64 (softmax, selection by score + bias with ties
+                         to the lower index, unbiased weights divided by their sum)
 """
 import json
+import math
 import os
+import struct
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
@@ -38,6 +44,43 @@ FIXTURES = {
         "inverse_scale_perm_single": [0, 1, 8, 9, 16, 17, 24, 25, 2, 3, 10, 11, 18, 19, 26, 27,
                                       4, 5, 12, 13, 20, 21, 28, 29, 6, 7, 14, 15, 22, 23, 30, 31],
     },
+}
+
+
+
+def _fp16(x: float) -> float:
+    return struct.unpack("<e", struct.pack("<e", x))[0]
+
+
+def _topk_softmax_f64(rows, bias, topk, renormalize):
+    ids, weights = [], []
+    for row in rows:
+        m = max(row)
+        ex = [math.exp(v - m) for v in row]
+        p = [v / sum(ex) for v in ex]
+        order = sorted(range(len(row)), key=lambda e: (-(p[e] + bias[e]), e))[:topk]
+        w = [p[e] for e in order]
+        if renormalize:
+            s = sum(w)
+            w = [v / s for v in w]
+        ids.append(order)
+        weights.append(w)
+    return ids, weights
+
+
+_GATING = [[_fp16(v) for v in r] for r in ([0.10, 0.80, -0.20, 0.30], [1.20, -0.40, 0.50, 0.10],
+                                           [-0.70, 0.60, 0.20, 1.10])]
+_BIAS = [struct.unpack("<f", struct.pack("<f", v))[0] for v in (0.05, -0.10, 0.20, 0.15)]
+_IDS, _WEIGHTS = _topk_softmax_f64(_GATING, _BIAS, 2, True)
+FIXTURES["topk_softmax_kat.json"] = {
+    "source": "inputs: tests/test_marlin_moe.py:248-272; expected: float64 closed form",
+    "gating_fp16_values": _GATING,
+    "bias": _BIAS,
+    "topk": 2,
+    "renormalize": True,
+    "topk_ids": _IDS,
+    "topk_weights": _WEIGHTS,
+    "token_expert_indices": [[t + j * 3 for j in range(2)] for t in range(3)],
 }
 
 if __name__ == "__main__":

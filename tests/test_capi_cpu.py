@@ -129,3 +129,27 @@ def test_moe_align_rejections():
     st = lib.marlin_moe_align_block_size(16, capi.F32, 8, 8, 16, 16, 100, 16, 10, 16, None, 0,
                                          None)
     assert st == 1 and "int32 or int64" in lib.marlin_get_last_error().decode()
+
+
+def test_topk_router_rejections():
+    lib = capi.load()
+
+    def call(fn, ids_dt=capi.I32, k=2, g_dt=capi.F16, t=4, e=8, bias_numel=0):
+        bias = 16 if bias_numel else None
+        st = fn(16, 16, ids_dt, 16, k, 16, g_dt, t, e, 1, bias, bias_numel, None)
+        return st, lib.marlin_get_last_error().decode()
+
+    for fn in (lib.marlin_topk_softmax, lib.marlin_topk_sigmoid):
+        st, err = call(fn, bias_numel=7)
+        assert st == 1 and "bias size mismatch, expected: 8" in err
+        st, err = call(fn, g_dt=capi.I32)
+        assert st == 1 and "Unsupported gating_output data type" in err
+        st, err = call(fn, ids_dt=capi.F32)
+        assert st == 1 and "int32, uint32 or int64" in err
+        st, err = call(fn, k=9)
+        assert st == 1 and "topk" in err
+        st, err = call(fn, e=8192, k=2)
+        assert st == 2 and "experts" in err
+        st, err = call(fn, e=1024, k=300)
+        assert st == 2 and "topk <= 256" in err
+        assert call(fn, t=0)[0] == 0  # no tokens: nothing to launch

@@ -312,3 +312,80 @@ def test_moe_sum_rounding_modes():
     assert torch.equal(O.moe_sum(x2), (x2[:, 0].float() + x2[:, 1].float()).to(torch.bfloat16))
     # top-k 1: a copy
     assert torch.equal(O.moe_sum(x2[:, :1]), x2[:, 0])
+
+
+# ---- MoE router (topk_softmax / topk_sigmoid) --------------------------------------------
+
+def test_topk_softmax_reference_kat():
+    g = _golden("topk_softmax_kat.json")
+    gating = np.asarray(g["gating_fp16_values"], dtype=np.float16)
+    w, ids, tei = O.topk_gating(gating, g["topk"], g["renormalize"], np.asarray(g["bias"]))
+    assert ids.tolist() == g["topk_ids"]
+    assert tei.tolist() == g["token_expert_indices"]
+    np.testing.assert_allclose(w, np.asarray(g["topk_weights"]), rtol=0, atol=1e-6)
+
+
+def test_topk_closed_forms_and_tie_rule():
+    ln2, ln3 = math.log(2.0), math.log(3.0)
+    # probabilities [3, 1, 2, 2] / 8: the tie between experts 2 and 3 goes to 2
+    x = np.array([[ln3, 0.0, ln2, ln2]], dtype=np.float32)
+    w, ids, _ = O.topk_gating(x, 2)
+    assert ids.tolist() == [[0, 2]]
+    np.testing.assert_allclose(w, [[0.375, 0.25]], atol=1e-7)
+    w, ids, _ = O.topk_gating(x, 2, renormalize=True)
+    np.testing.assert_allclose(w, [[0.6, 0.4]], atol=1e-7)
+    # a bias moves the choice but the weights stay the unbiased probabilities
+    w, ids, _ = O.topk_gating(x, 2, True, np.array([-0.2, 0, 0, 0], np.float32))
+    assert ids.tolist() == [[2, 3]]
+    np.testing.assert_allclose(w, [[0.5, 0.5]], atol=1e-7)
+    w, ids, _ = O.topk_gating(x, 2, False, np.array([0, 0, 0, 0.01], np.float32))
+    assert ids.tolist() == [[0, 3]]
+    np.testing.assert_allclose(w, [[0.375, 0.25]], atol=1e-7)
+    # sigmoid(0) = 1/2, sigmoid(ln 3) = 3/4, sigmoid(-ln 3) = 1/4
+    x = np.array([[0.0, ln3, -ln3]], dtype=np.float32)
+    w, ids, _ = O.topk_gating(x, 2, scoring="sigmoid")
+    assert ids.tolist() == [[1, 0]]
+    np.testing.assert_allclose(w, [[0.75, 0.5]], atol=1e-7)
+    w, ids, _ = O.topk_gating(x, 2, True, scoring="sigmoid")
+    np.testing.assert_allclose(w, [[0.6, 0.4]], atol=1e-7)
+    # all-equal row: experts in index order
+    w, ids, tei = O.topk_gating(np.zeros((2, 5), np.float32), 5)
+    assert ids.tolist() == [[0, 1, 2, 3, 4]] * 2
+    assert tei.tolist() == [[0, 2, 4, 6, 8], [1, 3, 5, 7, 9]]
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_topk_invariants(seed):
+    rng = np.random.default_rng(seed)
+    t, e, k = 33, 96, 6
+    x = rng.standard_normal((t, e)).astype(np.float32)
+    bias = (0.01 * rng.standard_normal(e)).astype(np.float32)
+    w, ids, _ = O.topk_gating(x, k, False, bias)
+    p = torch.softmax(torch.from_numpy(x), dim=-1).numpy()  # library softmax
+    choice = p + bias
+    for r in range(t):
+        sel = ids[r].astype(np.int64)
+        assert len(set(sel.tolist())) == k
+        assert np.all(np.diff(choice[r, sel]) <= 1e-7)  # non-increasing choice
+        rest = np.setdiff1d(np.arange(e), sel)
+        assert choice[r, rest].max() <= choice[r, sel].min() + 1e-7
+    np.testing.assert_allclose(w, np.take_along_axis(p, ids.astype(np.int64), 1), rtol=1e-6)
+    # renormalized weights sum to one; softmax is shift invariant
+    w2, ids2, _ = O.topk_gating(x + 3.0, k, True, bias)
+    assert np.array_equal(ids2, ids)
+    np.testing.assert_allclose(w2.sum(axis=1), 1.0, rtol=1e-6)
+    # k = E lists every expert once
+    _, ids3, _ = O.topk_gating(x[:4, :16], 16)
+    assert all(sorted(r) == list(range(16)) for r in ids3.tolist())
+
+
+def test_planted_biased_router_weights_are_caught():
+    g = _golden("topk_softmax_kat.json")
+    gating = np.asarray(g["gating_fp16_values"], dtype=np.float16).astype(np.float32)
+    bias = np.asarray(g["bias"], dtype=np.float32)
+    _, ids, _ = O.topk_gating(gating, 2, True, bias)
+    # the plausible slip: returning the biased choice score as the weight
+    p = torch.softmax(torch.from_numpy(gating), dim=-1).numpy() + bias
+    wrong = np.take_along_axis(p, ids.astype(np.int64), 1)
+    wrong = wrong / wrong.sum(axis=1, keepdims=True)
+    assert np.abs(wrong - np.asarray(g["topk_weights"])).max() > 1e-3
