@@ -250,8 +250,10 @@ def moe_case(key, tokens, steps, warmup, seed):
             "vs_roofline": round(t / roof, 3)}
 
 
-def router_case(key, tokens, steps, warmup, seed):
-    """cfg5 router: topk_softmax over fp32 logits [T, 256], top-8, renormalized."""
+def router_case(key, tokens, steps, warmup, seed, grouped=False):
+    """cfg5 router: topk_softmax over fp32 logits [T, 256], top-8, renormalized.  grouped:
+    grouped_topk at the DeepSeek-V3 routing shape (256 experts in 8 groups, keep 4, top-8,
+    sigmoid + fp32 bias, renormalized, scale 2.5) on the same logits."""
     import torch
 
     from marlin_v100_amd import _custom_ops as ops
@@ -259,12 +261,16 @@ def router_case(key, tokens, steps, warmup, seed):
     E, topk = 256, 8
     gen = torch.Generator(device="cuda").manual_seed(seed)
     logits = torch.randn((tokens, E), generator=gen, device="cuda")
+    bias = torch.randn(E, generator=gen, device="cuda") * 0.1
     w = torch.empty((tokens, topk), dtype=torch.float32, device="cuda")
     ids = torch.empty((tokens, topk), dtype=torch.int32, device="cuda")
     tei = torch.empty((tokens, topk), dtype=torch.int32, device="cuda")
 
     def fn():
-        ops.topk_softmax(w, ids, tei, logits, True, None)
+        if grouped:
+            ops.grouped_topk(logits, 8, 4, topk, True, 2.5, bias, 1)
+        else:
+            ops.topk_softmax(w, ids, tei, logits, True, None)
 
     # eager calls are bound by host dispatch (torch op -> C ABI -> launch); the device rate
     # comes from a captured graph of 50 back-to-back calls (the kernel writes no memset node)
@@ -374,10 +380,11 @@ def main() -> int:
                 continue
             configs[key] = moe_case(key, t, max(10, args.steps // 10), max(3, args.warmup // 4), 1005)
             print(f"# {key}: {configs[key]['layer_us']} us", file=sys.stderr, flush=True)
-        for key, t in (("cfg5_router_t16", 16), ("cfg5_router_t2048", 2048)):
+        for key, t, grouped in (("cfg5_router_t16", 16, False), ("cfg5_router_t2048", 2048, False),
+                                ("router_grouped_topk_t2048", 2048, True)):
             if only and key not in only:
                 continue
-            configs[key] = router_case(key, t, args.steps, args.warmup, 1005)
+            configs[key] = router_case(key, t, args.steps, args.warmup, 1005, grouped)
             print(f"# {key}: {configs[key]['us']} us", file=sys.stderr, flush=True)
 
     t = head["us"] / 1e6

@@ -235,6 +235,28 @@ marlin_status_t marlin_topk_sigmoid(float* topk_weights, void* topk_indices,
                                     const float* bias, int64_t bias_numel,
                                     marlin_stream_t stream);
 
+/*
+ * Grouped MoE router.  scores: [num_tokens, num_experts] fp16, bf16 or fp32, contiguous; the
+ * experts form n_group equal groups.  Per row, with s = scores (scoring_func 0) or
+ * sigmoid(scores) (scoring_func 1) in fp32 and choice = s + bias (bias [num_experts] fp16,
+ * bf16 or fp32; non-finite inputs do not compete): a group's score is the sum of its two
+ * largest choices; the topk_group best groups are kept (ties to the lower group); the topk
+ * experts of the kept groups by choice follow (ties to the lower expert).
+ * topk_values [num_tokens, topk] fp32 = s * routed_scaling_factor, divided by
+ * (1e-20 + sum of the chosen s) when renormalize != 0; topk_indices [num_tokens, topk] int32.
+ * A row whose last kept group scores -inf gets experts 0..topk-1 with weight 1/topk.
+ * This build supports num_experts <= 1024 (MARLIN_STATUS_NOT_SUPPORTED beyond).
+ * Replaces torch.ops._moe_C.grouped_topk (reference csrc/moe/grouped_topk_kernels.cu:987-1090;
+ * schema csrc/moe/torch_bindings_marlin.cpp:48-54).
+ */
+marlin_status_t marlin_grouped_topk(const void* scores, marlin_dtype_t scores_dtype,
+                                    int64_t num_tokens, int64_t num_experts, int64_t n_group,
+                                    int64_t topk_group, int64_t topk, int renormalize,
+                                    double routed_scaling_factor, const void* bias,
+                                    marlin_dtype_t bias_dtype, int64_t bias_numel,
+                                    int64_t scoring_func, float* topk_values,
+                                    int32_t* topk_indices, marlin_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

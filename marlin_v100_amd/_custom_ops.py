@@ -1,5 +1,5 @@
 """Python op wrappers with the reference's names and signatures
-(reference vllm/_custom_ops.py:1163-1351, 2129-2168, 2286-2318, 2361-2483).
+(reference vllm/_custom_ops.py:1163-1351, 2129-2168, 2286-2358, 2361-2483).
 
 Each wrapper forwards to the torch op registered by _C.so / _moe_C.so, which validates the
 arguments and calls the C ABI of libmarlin_mi355x.so.  Fake (meta) implementations let
@@ -114,6 +114,20 @@ def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
                  e_score_correction_bias: torch.Tensor | None = None) -> None:
     torch.ops._moe_C.topk_sigmoid(topk_weights, topk_ids, token_expert_indices, gating_output,
                                   renormalize, e_score_correction_bias)
+
+
+def grouped_topk(scores: torch.Tensor, num_expert_group: int, topk_group: int, topk: int,
+                 renormalize: bool, routed_scaling_factor: float, bias: torch.Tensor,
+                 scoring_func: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    return torch.ops._moe_C.grouped_topk(scores, num_expert_group, topk_group, topk,
+                                         renormalize, routed_scaling_factor, bias, scoring_func)
+
+
+@register_fake("_moe_C::grouped_topk")
+def _grouped_topk_fake(scores, n_group, topk_group, topk, renormalize, routed_scaling_factor,
+                       bias, scoring_func):
+    return (torch.empty((scores.shape[0], topk), dtype=torch.float32, device=scores.device),
+            torch.empty((scores.shape[0], topk), dtype=torch.int32, device=scores.device))
 
 
 def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: int,

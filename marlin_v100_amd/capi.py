@@ -53,6 +53,8 @@ SIGNATURES = {
     "marlin_silu_and_mul": (_I, [_P, _I, _I64, _I64, _P, _P]),
     "marlin_topk_softmax": (_I, [_P, _P, _I, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I64, _P]),
     "marlin_topk_sigmoid": (_I, [_P, _P, _I, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I64, _P]),
+    "marlin_grouped_topk": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I, ctypes.c_double, _P,
+                                 _I, _I64, _I64, _P, _P, _P]),
 }
 
 _lib = None
@@ -200,3 +202,16 @@ def topk_gating(gating, topk, renormalize=False, bias=None, scoring="softmax",
     _check(fn(_ptr(w), _ptr(ids), _DT[ids_dtype], _ptr(tei), topk, _ptr(gating), _dt(gating), t,
               e, int(renormalize), _ptr(bias), _numel(bias), _stream()))
     return w, ids, tei
+
+
+def grouped_topk(scores, n_group, topk_group, topk, renormalize, routed_scaling_factor, bias,
+                 scoring_func=0):
+    """Grouped router over scores [T, E]: returns (values f32 [T, topk], ids i32 [T, topk])."""
+    t, e = scores.shape
+    vals = torch.empty((t, topk), dtype=torch.float32, device=scores.device)
+    ids = torch.empty((t, topk), dtype=torch.int32, device=scores.device)
+    _check(load().marlin_grouped_topk(_ptr(scores), _dt(scores), t, e, n_group, topk_group, topk,
+                                      int(renormalize), float(routed_scaling_factor), _ptr(bias),
+                                      _dt(bias), _numel(bias), scoring_func, _ptr(vals),
+                                      _ptr(ids), _stream()))
+    return vals, ids

@@ -968,4 +968,46 @@ marlin_status_t marlin_topk_sigmoid(float* topk_weights, void* topk_indices,
                      bias, bias_numel, stream);
 }
 
+marlin_status_t marlin_grouped_topk(const void* scores, marlin_dtype_t scores_dtype,
+                                    int64_t num_tokens, int64_t num_experts, int64_t n_group,
+                                    int64_t topk_group, int64_t topk, int renormalize,
+                                    double routed_scaling_factor, const void* bias,
+                                    marlin_dtype_t bias_dtype, int64_t bias_numel,
+                                    int64_t scoring_func, float* topk_values,
+                                    int32_t* topk_indices, marlin_stream_t stream) {
+  return guarded([&] {
+    const auto half_or_f32 = [](marlin_dtype_t d) {
+      return d == MARLIN_DTYPE_FLOAT16 || d == MARLIN_DTYPE_BFLOAT16 || d == MARLIN_DTYPE_FLOAT32;
+    };
+    check(half_or_f32(scores_dtype), "Invalid dtype, only supports float16, float32, and bfloat16");
+    check(half_or_f32(bias_dtype),
+          "Invalid bias dtype, only supports float16, float32, and bfloat16");
+    check(num_tokens >= 0 && num_experts > 0, "invalid scores shape");
+    check(n_group > 0, "n_group must be positive");
+    check(topk > 0, "topk must be positive");
+    check(topk_group > 0, "topk_group must be positive");
+    check(topk_group <= n_group, "topk_group must be <= n_group");
+    check(num_experts % n_group == 0, "num_experts should be divisible by n_group");
+    check(n_group <= 32, "n_group should be smaller than or equal to 32 for now");
+    check(topk <= 32, "topk should be smaller than or equal to 32 for now");
+    check(topk <= topk_group * (num_experts / n_group),
+          "topk must be <= topk_group * (num_experts / n_group)");
+    check(scoring_func == 0 || scoring_func == 1,
+          "scoring_func must be SCORING_NONE (0) or SCORING_SIGMOID (1)");
+    check(bias_numel == num_experts, "bias size mismatch, expected: ", num_experts);
+    check_supported(num_experts <= kGroupedMaxExperts, "this build supports at most ",
+                    kGroupedMaxExperts, " experts for grouped_topk");
+    if (num_tokens == 0) return;
+    check(scores && bias && topk_values && topk_indices, "null tensor pointer");
+    const auto kind = [](marlin_dtype_t d) {
+      return d == MARLIN_DTYPE_FLOAT16 ? 0 : d == MARLIN_DTYPE_BFLOAT16 ? 1 : 2;
+    };
+    check_hip(launch_grouped_topk((int)scoring_func, kind(scores_dtype), kind(bias_dtype), scores,
+                                  bias, topk_values, topk_indices, num_tokens, (int)num_experts,
+                                  (int)n_group, (int)topk_group, (int)topk, renormalize != 0,
+                                  (float)routed_scaling_factor, (hipStream_t)stream),
+              "grouped_topk launch");
+  });
+}
+
 }  // extern "C"

@@ -31,6 +31,12 @@ constexpr int kMaxK = 256;
 hipError_t launch_topk_gating(bool sigmoid, int in_kind, const void* gating, const float* bias,
                               float* weights, void* ids, int ids_kind, int* tei, int64_t T, int E,
                               int k, bool renorm, hipStream_t stream);
+// grouped_topk: scoring 0 none / 1 sigmoid; bias_kind like in_kind; E <= kGroupedMaxExperts.
+constexpr int kGroupedMaxExperts = 1024;
+hipError_t launch_grouped_topk(int scoring, int in_kind, int bias_kind, const void* scores,
+                               const void* bias, float* values, int* ids, int64_t T, int E,
+                               int n_group, int topk_group, int k, bool renorm, float rsf,
+                               hipStream_t stream);
 
 // One GEMM launch configuration.
 struct GemmLaunch {

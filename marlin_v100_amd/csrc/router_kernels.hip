@@ -13,6 +13,7 @@
 // cross-lane operations (DPP, permlane swaps).  No LDS, no workspace: the reference's E > 256 / non-power-of-two path goes through a
 // [T, E] fp32 workspace (:774-777); here every E <= 64 * 64 stays in registers.
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.h"
 #include "host_common.h"
@@ -130,7 +131,8 @@ __device__ __forceinline__ float wave_sum(float v) {
   return p.v0 + p.v1;
 }
 
-constexpr int kSoftmax = 0;
+constexpr int kSoftmax = 0;  // topk_gating scoring
+constexpr int kScoreNone = 0;  // grouped_topk scoring_func 0: the scores as given
 constexpr int kSigmoid = 1;
 constexpr int kWavesPerBlock = 4;
 
@@ -238,6 +240,174 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void topk_gating_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// grouped_topk (reference csrc/moe/grouped_topk_kernels.cu:517-657, host :987-1090): the
+// experts form n_group equal groups; a group's score is the sum of its two largest
+// score + bias values (:469-512); the topk_group best groups are kept (ties to the lower
+// group, :576-585); the top-k experts of the kept groups by score + bias follow (ties to the
+// lower expert); weights are the unbiased scores times routed_scaling_factor, divided by
+// (1e-20 + their sum) when renormalizing (:639-656).  If the last kept group's score is -inf
+// the row falls back to experts 0..k-1 with weight 1/k (:587-600).  Inputs that are not
+// finite do not compete (their choice is -inf, :623-628).
+// Scores are computed in fp32 (the reference test oracle's arithmetic,
+// tests/test_marlin_moe.py:136-191).  Choice values pass through LDS so that lane g can take
+// the top two of group g.
+// ---------------------------------------------------------------------------------------
+template <class BT>
+__device__ __forceinline__ float load_bias(const void* b, int e) {
+  if constexpr (std::is_same<BT, float>::value) return reinterpret_cast<const float*>(b)[e];
+  else return raw16_to_float(reinterpret_cast<const uint16_t*>(b)[e], BT{});
+}
+
+template <class IT, class BT, int VPL, int SF>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void grouped_topk_kernel(
+    const typename ScoreIn<IT>::raw* __restrict__ scores_in, const void* __restrict__ bias,
+    float* __restrict__ values, int* __restrict__ ids, int64_t num_tokens, int num_experts,
+    int n_group, int topk_group, int k, int renormalize, float routed_scaling_factor) {
+  __shared__ float choice_lds[kWavesPerBlock][kGroupedMaxExperts];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  if (t >= num_tokens) return;  // whole wave; LDS is per wave, no barriers below
+  const typename ScoreIn<IT>::raw* row = scores_in + t * num_experts;
+  const int epg = num_experts / n_group;
+
+  float score[VPL];
+  float choice[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    float x = e < num_experts ? ScoreIn<IT>::get(row, e) : 0.0f;
+    const bool finite = e < num_experts && __builtin_isfinite(x);
+    if constexpr (SF == kSigmoid) x = 1.0f / (1.0f + expf(-x));
+    score[j] = x;
+    choice[j] = finite ? x + load_bias<BT>(bias, e) : -INFINITY;
+    if (e < num_experts) choice_lds[wave][e] = choice[j];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // group scores: lane g < n_group sums the two largest choices of group g
+  float gscore = -INFINITY;
+  if (lane < n_group) {
+    float m1 = -INFINITY, m2 = -INFINITY;
+    const float* grp = &choice_lds[wave][lane * epg];
+    for (int i = 0; i < epg; ++i) {
+      const float v = grp[i];
+      if (v > m1) {
+        m2 = m1;
+        m1 = v;
+      } else if (v > m2) {
+        m2 = v;
+      }
+    }
+    gscore = epg >= 2 ? m1 + m2 : m1;
+  }
+  uint32_t kept = 0;  // wave-uniform bitmask of kept groups
+  float last = 0.0f;
+  bool glive = lane < n_group;
+  for (int r = 0; r < topk_group; ++r) {
+    float v = glive ? gscore : -INFINITY;
+    int g = glive ? lane : 64 + lane;  // spent and absent lanes lose every tie
+    wave_argmax(v, g);
+    g = __builtin_amdgcn_readfirstlane(g);
+    kept |= 1u << (g & 31);
+    if (lane == g) glive = false;
+    last = v;
+  }
+  float* vrow = values + t * k;
+  int* irow = ids + t * k;
+  if (!(last > -INFINITY)) {
+    for (int r = lane; r < k; r += 64) {
+      irow[r] = r;
+      vrow[r] = 1.0f / (float)k;
+    }
+    return;
+  }
+
+  uint64_t live = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < num_experts && ((kept >> (e / epg)) & 1)) live |= 1ull << j;
+  }
+  float sum = 0.0f;
+  float kept_w = 0.0f;  // lane r keeps the unbiased score of round r (k <= 64)
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int bi = 1 << 30;
+    float bw = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (((live >> j) & 1) && (choice[j] > bv || bi == (1 << 30))) {
+        bv = choice[j];
+        bi = lane + 64 * j;
+        bw = score[j];
+      }
+    }
+    wave_argmax(bv, bi);
+    const int wi = __builtin_amdgcn_readfirstlane(bi);
+    const float w = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bw), wi & 63));
+    if ((wi & 63) == lane) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        if (j == (wi >> 6)) live &= ~(1ull << j);
+    }
+    sum += w;
+    if (lane == r) kept_w = w;
+    if (lane == 0) irow[r] = wi;
+  }
+  const float scale =
+      renormalize ? routed_scaling_factor / (1e-20f + sum) : routed_scaling_factor;
+  if (lane < k) vrow[lane] = kept_w * scale;
+}
+
+template <class IT, class BT, int SF>
+hipError_t launch_grouped_vpl(const void* scores, const void* bias, float* values, int* ids,
+                              int64_t T, int E, int n_group, int topk_group, int k, bool renorm,
+                              float rsf, hipStream_t stream) {
+  const dim3 grid((unsigned)((T + kWavesPerBlock - 1) / kWavesPerBlock));
+  const dim3 block(64 * kWavesPerBlock);
+  using R = typename ScoreIn<IT>::raw;
+  const R* g = reinterpret_cast<const R*>(scores);
+#define MMI_GROUPED_LAUNCH(V)                                                                 \
+  hipLaunchKernelGGL((grouped_topk_kernel<IT, BT, V, SF>), grid, block, 0, stream, g, bias,   \
+                     values, ids, T, E, n_group, topk_group, k, (int)renorm, rsf)
+  const int vpl = (E + 63) / 64;
+  if (vpl <= 1) MMI_GROUPED_LAUNCH(1);
+  else if (vpl <= 2) MMI_GROUPED_LAUNCH(2);
+  else if (vpl <= 4) MMI_GROUPED_LAUNCH(4);
+  else if (vpl <= 8) MMI_GROUPED_LAUNCH(8);
+  else MMI_GROUPED_LAUNCH(16);
+#undef MMI_GROUPED_LAUNCH
+  return hipGetLastError();
+}
+
+template <class IT, int SF>
+hipError_t launch_grouped_bias(int bias_kind, const void* scores, const void* bias,
+                               float* values, int* ids, int64_t T, int E, int n_group,
+                               int topk_group, int k, bool renorm, float rsf,
+                               hipStream_t stream) {
+  switch (bias_kind) {
+    case 0: return launch_grouped_vpl<IT, F16, SF>(scores, bias, values, ids, T, E, n_group, topk_group, k, renorm, rsf, stream);
+    case 1: return launch_grouped_vpl<IT, BF16, SF>(scores, bias, values, ids, T, E, n_group, topk_group, k, renorm, rsf, stream);
+    default: return launch_grouped_vpl<IT, float, SF>(scores, bias, values, ids, T, E, n_group, topk_group, k, renorm, rsf, stream);
+  }
+}
+
+template <int SF>
+hipError_t launch_grouped_in(int in_kind, int bias_kind, const void* scores, const void* bias,
+                             float* values, int* ids, int64_t T, int E, int n_group,
+                             int topk_group, int k, bool renorm, float rsf, hipStream_t stream) {
+  switch (in_kind) {
+    case 0: return launch_grouped_bias<F16, SF>(bias_kind, scores, bias, values, ids, T, E, n_group, topk_group, k, renorm, rsf, stream);
+    case 1: return launch_grouped_bias<BF16, SF>(bias_kind, scores, bias, values, ids, T, E, n_group, topk_group, k, renorm, rsf, stream);
+    default: return launch_grouped_bias<float, SF>(bias_kind, scores, bias, values, ids, T, E, n_group, topk_group, k, renorm, rsf, stream);
+  }
+}
+
 template <class IT, int SF, class OT>
 hipError_t launch_vpl(const void* gating, const float* bias, float* w, OT* ids, int* tei,
                       int64_t T, int E, int k, bool renorm, hipStream_t stream) {
@@ -289,6 +459,18 @@ hipError_t launch_topk_gating(bool sigmoid, int in_kind, const void* gating, con
   int32_t* o = reinterpret_cast<int32_t*>(ids);
   return sigmoid ? launch_in<kSigmoid>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream)
                  : launch_in<kSoftmax>(in_kind, gating, bias, weights, o, tei, T, E, k, renorm, stream);
+}
+
+hipError_t launch_grouped_topk(int scoring, int in_kind, int bias_kind, const void* scores,
+                               const void* bias, float* values, int* ids, int64_t T, int E,
+                               int n_group, int topk_group, int k, bool renorm, float rsf,
+                               hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  return scoring == kSigmoid
+             ? launch_grouped_in<kSigmoid>(in_kind, bias_kind, scores, bias, values, ids, T, E,
+                                           n_group, topk_group, k, renorm, rsf, stream)
+             : launch_grouped_in<kScoreNone>(in_kind, bias_kind, scores, bias, values, ids, T, E,
+                                           n_group, topk_group, k, renorm, rsf, stream);
 }
 
 }  // namespace mmi

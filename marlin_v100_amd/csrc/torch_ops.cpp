@@ -3,8 +3,8 @@
 // Built twice: with MMI_EXT_NAME=_C it registers torch.ops._C.{marlin_gemm,
 // gptq_marlin_repack, awq_marlin_repack} (schemas byte-identical to the reference
 // csrc/torch_bindings_marlin.cpp:6-21); with MMI_EXT_NAME=_moe_C it registers
-// torch.ops._moe_C.{topk_softmax, topk_sigmoid, moe_align_block_size, moe_wna16_marlin_gemm,
-// moe_sum} (csrc/moe/torch_bindings_marlin.cpp:5-47).  The _C build also registers the inspection op
+// torch.ops._moe_C.{topk_softmax, topk_sigmoid, grouped_topk, moe_align_block_size,
+// moe_wna16_marlin_gemm, moe_sum} (csrc/moe/torch_bindings_marlin.cpp:5-54).  The _C build also registers the inspection op
 // torch.ops._marlin_mi355x.dequantize.  Tensor-level checks (device, contiguity, ranks,
 // shapes) mirror the reference's TORCH_CHECKs; everything else is validated by the C ABI,
 // whose messages are rethrown unchanged.
@@ -440,6 +440,32 @@ void op_topk_gating(at::Tensor& topk_weights, at::Tensor& topk_indices,
              bias.has_value() ? bias->numel() : 0, cur_stream(gating_output)));
 }
 
+// reference grouped_topk (csrc/moe/grouped_topk_kernels.cu:987-1090): allocates and returns
+// (topk_values fp32, topk_indices int32), both [num_tokens, topk].
+std::tuple<at::Tensor, at::Tensor> op_grouped_topk(const at::Tensor& scores, int64_t n_group,
+                                                   int64_t topk_group, int64_t topk,
+                                                   bool renormalize,
+                                                   double routed_scaling_factor,
+                                                   const at::Tensor& bias,
+                                                   int64_t scoring_func) {
+  TORCH_CHECK(scores.dim() == 2, "scores must be a 2D Tensor");
+  TORCH_CHECK(scores.is_cuda() && scores.is_contiguous(), "scores must be a contiguous GPU tensor");
+  TORCH_CHECK(bias.is_cuda() && bias.is_contiguous() && bias.dim() == 1,
+              "bias must be a contiguous 1D GPU tensor");
+  const at::OptionalDeviceGuard guard(scores.device());
+  const int64_t num_tokens = scores.size(0);
+  auto values = torch::empty({num_tokens, std::max<int64_t>(topk, 0)},
+                             scores.options().dtype(at::kFloat));
+  auto indices = torch::empty({num_tokens, std::max<int64_t>(topk, 0)},
+                              scores.options().dtype(at::kInt));
+  rethrow(marlin_grouped_topk(scores.data_ptr(), to_mdt(scores.scalar_type()), num_tokens,
+                              scores.size(1), n_group, topk_group, topk, renormalize ? 1 : 0,
+                              routed_scaling_factor, bias.data_ptr(), to_mdt(bias.scalar_type()),
+                              bias.numel(), scoring_func, values.data_ptr<float>(),
+                              indices.data_ptr<int32_t>(), cur_stream(scores)));
+  return {values, indices};
+}
+
 TORCH_LIBRARY(_moe_C, m) {
   m.def(
       "topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! "
@@ -451,6 +477,12 @@ TORCH_LIBRARY(_moe_C, m) {
       "token_expert_indices, Tensor gating_output, bool renormalize, Tensor? "
       "bias) -> ()");
   m.impl("topk_sigmoid", torch::kCUDA, &op_topk_gating<true>);
+  m.def(
+      "grouped_topk(Tensor scores, int n_group, int "
+      "topk_group, int topk, bool renormalize, float "
+      "routed_scaling_factor, Tensor bias, int scoring_func) -> (Tensor, "
+      "Tensor)");
+  m.impl("grouped_topk", torch::kCUDA, &op_grouped_topk);
   m.def(
       "moe_align_block_size(Tensor topk_ids, int num_experts,"
       "                     int block_size, Tensor! sorted_token_ids,"

@@ -437,6 +437,53 @@ def topk_gating(gating: np.ndarray, topk: int, renormalize: bool = False,
     return w, ids, tei
 
 
+# ---------------------------------------------------------------------------------------
+# MoE grouped router: grouped_topk (reference test oracle tests/test_marlin_moe.py:136-191;
+# kernel rules csrc/moe/grouped_topk_kernels.cu: group score = sum of the two largest
+# score + bias :469-512, kept groups :576-585, non-finite inputs never compete :623-628,
+# weights = unbiased score * routed_scaling_factor / (1e-20 + sum) :639-656, fallback to
+# experts 0..k-1 with weight 1/k when the last kept group scores -inf :587-600)
+# ---------------------------------------------------------------------------------------
+
+def grouped_topk(scores: np.ndarray, n_group: int, topk_group: int, topk: int,
+                 renormalize: bool, routed_scaling_factor: float, bias: np.ndarray,
+                 scoring_func: int = 0):
+    """scores [T, E]; returns (values f32 [T, topk], ids i32 [T, topk])."""
+    x = np.asarray(scores, dtype=np.float32)
+    t, e = x.shape
+    epg = e // n_group
+    if scoring_func == 0:
+        unbiased = x
+    elif scoring_func == 1:
+        unbiased = (np.float32(1.0) / (np.float32(1.0) + np.exp(-x, dtype=np.float32))).astype(
+            np.float32)
+    else:
+        raise ValueError(scoring_func)
+    biased = np.where(np.isfinite(x), unbiased + np.asarray(bias, np.float32)[None, :],
+                      np.float32(-np.inf)).astype(np.float32)
+    values = np.empty((t, topk), dtype=np.float32)
+    ids = np.empty((t, topk), dtype=np.int32)
+    for r in range(t):
+        gsc = []
+        for g in range(n_group):
+            top = np.sort(biased[r, g * epg:(g + 1) * epg])[::-1][:min(2, epg)]
+            gsc.append((float(np.float32(top.sum(dtype=np.float32))), g))
+        kept = sorted(gsc, key=lambda it: (-it[0], it[1]))[:topk_group]
+        if not kept[-1][0] > -np.inf:
+            ids[r] = np.arange(topk)
+            values[r] = np.float32(1.0 / topk)
+            continue
+        cand = [(float(biased[r, ex]), ex) for _, g in kept for ex in range(g * epg, (g + 1) * epg)]
+        sel = [ex for _, ex in sorted(cand, key=lambda it: (-it[0], it[1]))[:topk]]
+        w = unbiased[r, sel].astype(np.float32)
+        scale = np.float32(routed_scaling_factor)
+        if renormalize:
+            scale = np.float32(scale / (np.float32(1e-20) + w.sum(dtype=np.float32)))
+        ids[r] = sel
+        values[r] = w * scale
+    return values, ids
+
+
 def max_abs_rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:
     """max|out - ref| / max|ref| (the BASELINE tolerance metric)."""
     ref = ref.to(torch.float32)

@@ -9,6 +9,10 @@ imported or executed): the values below are copied from the cited test assertion
                          top-2, renormalize); expected ids and weights evaluated here from the
                          closed form in float64 (softmax, selection by score + bias with ties
                          to the lower index, unbiased weights divided by their sum)
+  grouped_topk_kat.json: inputs of tests/test_marlin_moe.py:313-345 (fp32 scores, sigmoid,
+                         4 groups, keep 2, top-3, renormalize); expected ids and weights
+                         evaluated here from the closed form in float64 (group score = sum of
+                         the two largest sigmoid + bias, ties to the lower index)
 """
 import json
 import math
@@ -81,6 +85,47 @@ FIXTURES["topk_softmax_kat.json"] = {
     "topk_ids": _IDS,
     "topk_weights": _WEIGHTS,
     "token_expert_indices": [[t + j * 3 for j in range(2)] for t in range(3)],
+}
+
+
+def _f32(x: float) -> float:
+    return struct.unpack("<f", struct.pack("<f", x))[0]
+
+
+def _grouped_topk_f64(rows, bias, n_group, topk_group, topk, renormalize, scale):
+    ids, weights = [], []
+    for row in rows:
+        e = len(row)
+        epg = e // n_group
+        s = [1.0 / (1.0 + math.exp(-v)) for v in row]
+        c = [s[i] + bias[i] for i in range(e)]
+        gsc = [sum(sorted(c[g * epg:(g + 1) * epg], reverse=True)[:2]) for g in range(n_group)]
+        kept = sorted(range(n_group), key=lambda g: (-gsc[g], g))[:topk_group]
+        cand = [i for g in kept for i in range(g * epg, (g + 1) * epg)]
+        sel = sorted(cand, key=lambda i: (-c[i], i))[:topk]
+        w = [s[i] for i in sel]
+        tot = sum(w) if renormalize else 1.0
+        ids.append(sel)
+        weights.append([v * scale / tot for v in w])
+    return ids, weights
+
+
+_GSCORES = [[_f32(v) for v in r] for r in ([0.10, 0.80, -0.40, 0.20, 1.50, 0.30, -0.10, 0.70],
+                                           [0.90, -0.30, 0.40, 0.20, -0.60, 0.50, 1.10, 0.00])]
+_GBIAS = [_f32(v) for v in (0.05, 0.10, -0.05, 0.00, 0.20, -0.10, 0.15, 0.05)]
+_GIDS, _GWEIGHTS = _grouped_topk_f64(_GSCORES, _GBIAS, 4, 2, 3, True, 1.0)
+FIXTURES["grouped_topk_kat.json"] = {
+    "source": "inputs: tests/test_marlin_moe.py:313-345; expected: float64 closed form",
+    "scores": _GSCORES,
+    "bias": _GBIAS,
+    "num_expert_group": 4,
+    "topk_group": 2,
+    "topk": 3,
+    "renormalize": True,
+    "routed_scaling_factor": 1.0,
+    "scoring_func": 1,
+    "topk_ids": _GIDS,
+    "topk_weights": _GWEIGHTS,
 }
 
 if __name__ == "__main__":

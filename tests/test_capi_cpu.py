@@ -153,3 +153,24 @@ def test_topk_router_rejections():
         st, err = call(fn, e=1024, k=300)
         assert st == 2 and "topk <= 256" in err
         assert call(fn, t=0)[0] == 0  # no tokens: nothing to launch
+
+
+def test_grouped_topk_rejections():
+    lib = capi.load()
+
+    def call(scores_dt=capi.F32, bias_dt=capi.F32, e=16, ng=4, tg=2, k=2, sf=0, bias_numel=16):
+        st = lib.marlin_grouped_topk(16, scores_dt, 4, e, ng, tg, k, 1, 1.0, 16, bias_dt,
+                                     bias_numel, sf, 16, 16, None)
+        return st, lib.marlin_get_last_error().decode()
+
+    assert call(scores_dt=capi.I32)[1].startswith("Invalid dtype")
+    assert call(bias_dt=capi.I64)[1].startswith("Invalid bias dtype")
+    assert "divisible by n_group" in call(e=18, bias_numel=18)[1]
+    assert "topk_group must be <= n_group" in call(tg=5)[1]
+    assert "n_group should be smaller than or equal to 32" in call(e=64, ng=64, bias_numel=64)[1]
+    assert "topk should be smaller than or equal to 32" in call(e=256, k=33, bias_numel=256)[1]
+    assert "topk must be <= topk_group" in call(k=9)[1]
+    assert "scoring_func must be" in call(sf=2)[1]
+    assert "bias size mismatch" in call(bias_numel=15)[1]
+    st, err = call(e=2048, bias_numel=2048)
+    assert st == 2 and "1024" in err

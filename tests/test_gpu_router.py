@@ -142,3 +142,81 @@ def test_topk_baseline_routing_full_size():
     exact = _check(logits, 8, True, None, "softmax", w, ids, tei)
     assert exact >= 0.95 * 2048  # rows without a 1e-6 near-tie among the top 9
     np.testing.assert_allclose(w.sum(dim=1).cpu().numpy(), 1.0, rtol=2e-6)
+
+
+# ---- grouped_topk ------------------------------------------------------------------------
+
+def test_grouped_topk_reference_kat():
+    with open(os.path.join(GOLDEN, "grouped_topk_kat.json")) as f:
+        g = json.load(f)
+    scores = torch.tensor(g["scores"], dtype=torch.float32).cuda()
+    bias = torch.tensor(g["bias"], dtype=torch.float32).cuda()
+    args = (g["num_expert_group"], g["topk_group"], g["topk"], g["renormalize"],
+            g["routed_scaling_factor"])
+    vals, ids = capi.grouped_topk(scores, *args, bias, g["scoring_func"])
+    assert ids.cpu().tolist() == g["topk_ids"]
+    np.testing.assert_allclose(vals.cpu().numpy(), np.asarray(g["topk_weights"]), rtol=0,
+                               atol=1e-6)
+    from marlin_v100_amd import _custom_ops as ops
+    vals2, ids2 = ops.grouped_topk(scores, *args, bias, g["scoring_func"])
+    assert torch.equal(ids2, ids) and torch.equal(vals2, vals)
+
+
+GROUPED = [  # (T, E, n_group, topk_group, topk)
+    (16, 256, 8, 4, 8),      # DeepSeek-V3 shape
+    (33, 64, 8, 3, 6), (7, 96, 4, 2, 5), (5, 160, 32, 4, 4), (9, 1024, 16, 4, 32),
+    (4, 512, 1, 1, 22), (3, 8, 8, 8, 8), (2048, 256, 8, 4, 8),
+]
+
+
+@pytest.mark.parametrize("T,E,ng,tg,k", GROUPED)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("scoring", [0, 1])
+def test_grouped_topk_matches_oracle(T, E, ng, tg, k, dtype, scoring):
+    gen = torch.Generator().manual_seed(T + 7 * E + ng + k)
+    scores = torch.randn((T, E), generator=gen).to(dtype)
+    for renorm, bias_dtype, rsf in ((True, torch.float32, 1.0), (False, torch.bfloat16, 2.5)):
+        bias = (torch.randn(E, generator=gen) * 0.1).to(bias_dtype)
+        vals, ids = capi.grouped_topk(scores.cuda(), ng, tg, k, renorm, rsf, bias.cuda(),
+                                      scoring)
+        ref_v, ref_i = O.grouped_topk(scores.float().numpy(), ng, tg, k, renorm, rsf,
+                                      bias.float().numpy(), scoring)
+        ids = ids.cpu().numpy()
+        x = scores.float().numpy()
+        s = x if scoring == 0 else 1.0 / (1.0 + np.exp(-x))
+        c = s + bias.float().numpy()[None, :]
+        epg = E // ng
+        exact = 0
+        for r in range(T):
+            assert len(set(ids[r].tolist())) == k
+            np.testing.assert_allclose(c[r, ids[r]], c[r, ref_i[r]], rtol=0, atol=2e-6)
+            # ids must be exact unless a deciding rank is a near-tie: the group scores around
+            # the topk_group cut, or the choices around the topk cut inside the kept groups
+            gs = np.sort([np.sort(c[r, g * epg:(g + 1) * epg])[-2:].sum() for g in range(ng)])
+            kept = sorted({int(i) // epg for i in ref_i[r]})
+            cand = np.sort(np.concatenate([c[r, g * epg:(g + 1) * epg] for g in kept]))
+            if (np.all(np.abs(np.diff(gs[::-1][:tg + 1])) > 1e-6) and
+                    np.all(np.abs(np.diff(cand[::-1][:k + 1])) > 1e-6)):
+                assert ids[r].tolist() == ref_i[r].tolist(), f"row {r}"
+                exact += 1
+        w = np.take_along_axis(s, ids.astype(np.int64), 1) * rsf
+        if renorm:
+            w = w / (1e-20 + np.take_along_axis(s, ids.astype(np.int64), 1).sum(1, keepdims=True))
+        np.testing.assert_allclose(vals.cpu().numpy(), w, rtol=1e-5, atol=1e-6)
+        if dtype == torch.float32:
+            assert exact >= 0.9 * T
+
+
+def test_grouped_topk_fallback_and_errors():
+    # every input non-finite: no group scores above -inf, experts 0..k-1 with weight 1/k
+    scores = torch.full((3, 16), float("inf"), device="cuda")
+    vals, ids = capi.grouped_topk(scores, 4, 2, 4, True, 1.0, torch.zeros(16, device="cuda"), 1)
+    assert ids.cpu().tolist() == [[0, 1, 2, 3]] * 3
+    np.testing.assert_allclose(vals.cpu().numpy(), 0.25)
+    from marlin_v100_amd import _custom_ops as ops
+    with pytest.raises(RuntimeError, match="num_experts should be divisible by n_group"):
+        ops.grouped_topk(torch.randn((2, 10), device="cuda"), 4, 2, 2, True, 1.0,
+                         torch.zeros(10, device="cuda"), 0)
+    with pytest.raises(RuntimeError, match="topk_group must be <= n_group"):
+        ops.grouped_topk(torch.randn((2, 16), device="cuda"), 4, 5, 2, True, 1.0,
+                         torch.zeros(16, device="cuda"), 0)

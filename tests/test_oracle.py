@@ -389,3 +389,70 @@ def test_planted_biased_router_weights_are_caught():
     wrong = np.take_along_axis(p, ids.astype(np.int64), 1)
     wrong = wrong / wrong.sum(axis=1, keepdims=True)
     assert np.abs(wrong - np.asarray(g["topk_weights"])).max() > 1e-3
+
+
+# ---- MoE grouped router (grouped_topk) ---------------------------------------------------
+
+def test_grouped_topk_reference_kat():
+    g = _golden("grouped_topk_kat.json")
+    vals, ids = O.grouped_topk(np.asarray(g["scores"], np.float32), g["num_expert_group"],
+                               g["topk_group"], g["topk"], g["renormalize"],
+                               g["routed_scaling_factor"], np.asarray(g["bias"], np.float32),
+                               g["scoring_func"])
+    assert ids.tolist() == g["topk_ids"]
+    np.testing.assert_allclose(vals, np.asarray(g["topk_weights"]), rtol=0, atol=1e-6)
+
+
+def test_grouped_topk_closed_forms():
+    # scoring 0 (scores as given): groups {0,1} {2,3} {4,5}; group scores 0.9, 1.1, 0.7
+    x = np.array([[0.5, 0.4, 1.0, 0.1, 0.6, 0.1]], np.float32)
+    z = np.zeros(6, np.float32)
+    vals, ids = O.grouped_topk(x, 3, 1, 2, False, 2.5, z, 0)
+    assert ids.tolist() == [[2, 3]]  # only group 1 kept, although expert 4 beats expert 3
+    np.testing.assert_allclose(vals, [[2.5, 0.25]], atol=1e-7)
+    vals, ids = O.grouped_topk(x, 3, 2, 3, True, 1.0, z, 0)
+    assert ids.tolist() == [[2, 0, 1]]  # groups 1 and 0 kept
+    np.testing.assert_allclose(vals, [[1.0 / 1.9, 0.5 / 1.9, 0.4 / 1.9]], rtol=1e-6)
+    # equal group scores: the lower group wins; a -inf kept group means the 1/k fallback
+    vals, ids = O.grouped_topk(np.zeros((1, 4), np.float32), 2, 1, 2, False, 1.0,
+                               np.zeros(4, np.float32), 0)
+    assert ids.tolist() == [[0, 1]]
+    vals, ids = O.grouped_topk(np.full((1, 4), np.inf, np.float32), 2, 1, 2, True, 1.0,
+                               np.zeros(4, np.float32), 1)
+    assert ids.tolist() == [[0, 1]]
+    np.testing.assert_allclose(vals, [[0.5, 0.5]])
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_grouped_topk_brute_force(seed):
+    # tiny rows: every choice of kept groups is enumerated; the kept set must be the one with
+    # the largest group scores and the experts the best choices inside it
+    import itertools
+    rng = np.random.default_rng(seed)
+    t, e, n_group, topk_group, k = 6, 12, 4, 2, 4
+    x = rng.standard_normal((t, e)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(e)).astype(np.float32)
+    vals, ids = O.grouped_topk(x, n_group, topk_group, k, True, 1.5, bias, 1)
+    s = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    c = s + bias
+    epg = e // n_group
+    for r in range(t):
+        gs = [np.sort(c[r, g * epg:(g + 1) * epg])[-2:].sum() for g in range(n_group)]
+        best = max(itertools.combinations(range(n_group), topk_group),
+                   key=lambda sub: sum(gs[g] for g in sub))
+        cand = [i for g in best for i in range(g * epg, (g + 1) * epg)]
+        want = sorted(cand, key=lambda i: -c[r, i])[:k]
+        assert ids[r].tolist() == want
+        np.testing.assert_allclose(vals[r], 1.5 * s[r, want] / s[r, want].sum(), rtol=1e-6)
+
+
+def test_planted_grouped_topk_top1_group_score_is_caught():
+    # the plausible slip: scoring a group by its best expert alone.  On the closed-form row the
+    # top-2 sums keep groups {1, 0} while best-expert scores would keep {1, 2}, so
+    # test_grouped_topk_closed_forms fails for an oracle with that slip.
+    x = np.array([0.5, 0.4, 1.0, 0.1, 0.6, 0.1], np.float32)
+    top1 = sorted(range(3), key=lambda g: (-x[2 * g:2 * g + 2].max(), g))[:2]
+    top2 = sorted(range(3), key=lambda g: (-np.sort(x[2 * g:2 * g + 2]).sum(), g))[:2]
+    assert top2 == [1, 0] and top1 == [1, 2]
+    _, ids = O.grouped_topk(x[None, :], 3, 2, 3, True, 1.0, np.zeros(6, np.float32), 0)
+    assert sorted({i // 2 for i in ids[0].tolist()}) == sorted(top2)
