@@ -202,7 +202,8 @@ int env_int(const char* name, int dflt) {
 //    resident in one round -- a second, partial round would stream its weights alone at the
 //    end -- and spread evenly over the CUs: each CU takes the same number of whole column
 //    groups and the groups left over are split along K into about one small block per CU.
-//    With at most half as many 64-column groups as CUs the groups are 32 columns wide; K is split across
+//    With at most half as many 64-column groups as CUs the groups are 32 columns wide, and
+//    16 columns wide when that many 16-column groups still fit one per CU; K is split across
 //    blocks only when under a quarter of the CUs would have a group, within an atomics budget.
 //  * 16 < M <= 32 is still weight bound: 32-row blocks with split-K until the grid holds
 //    about 4 workgroups per CU.
@@ -224,6 +225,9 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // workgroups, no cross-workgroup split; cfg1 4096x4096: 6.9 us against 12.7 us with
     // split K; N = 14336, 224 groups, stays at 64 columns: 9.5 against 11.9 us)
     if (int_operand && N / 64 <= cus / 2) nt = 2, depth = 4, occ = 1;
+    // with no more 16-column groups than CUs, 16-column groups keep every CU streaming
+    // (cfg1 4096x4096: 6.1 us against 6.8 us with 32-column groups on half the CUs)
+    if (int_operand && N % 16 == 0 && N / 16 <= cus) nt = 1, depth = 4, occ = 1;
     if (const char* t = getenv("MARLIN_MI355X_DECODE")) {
       sscanf(t, "%d,%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit, &occ);
     } else if (occ == 3) {

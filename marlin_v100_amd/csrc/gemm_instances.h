@@ -46,6 +46,9 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     MMI_DECODE(4, 4, 2, true, true, 1)
     MMI_DECODE(4, 3, 1, true, true, 1)
     MMI_DECODE(4, 4, 1, true, true, 1)
+    if constexpr (FMT != FMT_MXFP4 && FMT != FMT_NVFP4 && GSM != GSM_SMALL) {
+      MMI_DECODE(1, 4, 4, true, false, 1)  // 16-column groups: small N at M <= 16
+    }
 #undef MMI_DECODE
     return hipErrorInvalidValue;
   }
