@@ -244,7 +244,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void topk_gating_kernel(
 // grouped_topk (reference csrc/moe/grouped_topk_kernels.cu:517-657, host :987-1090): the
 // experts form n_group equal groups; a group's score is the sum of its two largest
 // score + bias values (:469-512); the topk_group best groups are kept (ties to the lower
-// group, :576-585); the top-k experts of the kept groups by score + bias follow (ties to the
+// group, :576-585; here by counting, per group lane, the groups that beat it); the top-k experts of the kept groups by score + bias follow (ties to the
 // lower expert); weights are the unbiased scores times routed_scaling_factor, divided by
 // (1e-20 + their sum) when renormalizing (:639-656).  If the last kept group's score is -inf
 // the row falls back to experts 0..k-1 with weight 1/k (:587-600).  Inputs that are not
@@ -304,21 +304,27 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void grouped_topk_kernel(
     }
     gscore = epg >= 2 ? m1 + m2 : m1;
   }
-  uint32_t kept = 0;  // wave-uniform bitmask of kept groups
-  float last = 0.0f;
-  bool glive = lane < n_group;
-  for (int r = 0; r < topk_group; ++r) {
-    float v = glive ? gscore : -INFINITY;
-    int g = glive ? lane : 64 + lane;  // spent and absent lanes lose every tie
-    wave_argmax(v, g);
-    g = __builtin_amdgcn_readfirstlane(g);
-    kept |= 1u << (g & 31);
-    if (lane == g) glive = false;
-    last = v;
+  // keep the topk_group best groups: lane g counts the groups that beat it (a larger score,
+  // or an equal score and a lower index) and is kept when fewer than topk_group do
+  __shared__ float gscore_lds[kWavesPerBlock][32];
+  if (lane < n_group) gscore_lds[wave][lane] = gscore;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int rank = 64;
+  if (lane < n_group) {
+    rank = 0;
+    for (int h = 0; h < n_group; ++h) {
+      const float o = gscore_lds[wave][h];
+      rank += (o > gscore || (o == gscore && h < lane)) ? 1 : 0;
+    }
   }
+  const uint32_t kept = (uint32_t)__ballot(rank < topk_group);  // wave-uniform group mask
+  // the last kept group scores -inf exactly when fewer than topk_group groups score above -inf
+  const int finite_groups = __popcll(__ballot(lane < n_group && gscore > -INFINITY));
   float* vrow = values + t * k;
   int* irow = ids + t * k;
-  if (!(last > -INFINITY)) {
+  if (finite_groups < topk_group) {
     for (int r = lane; r < k; r += 64) {
       irow[r] = r;
       vrow[r] = 1.0f / (float)k;
