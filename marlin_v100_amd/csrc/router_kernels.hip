@@ -9,8 +9,9 @@
 //
 // Layout on MI355X: one 64-lane wavefront per token.  Lane l holds experts l + 64*j for
 // j < VPL in registers, so each j is one coalesced 64-element load of the row; the softmax
-// max / sum and each of the k argmax steps are reductions across the wave in VALU
-// cross-lane operations (DPP, permlane swaps).  No LDS, no workspace: the reference's E > 256 / non-power-of-two path goes through a
+// max / sum are reductions across the wave in VALU cross-lane operations (DPP, permlane
+// swaps), and the top k are chosen by a threshold search over ballots (choose_topk) instead
+// of k dependent argmax rounds.  No workspace: the reference's E > 256 / non-power-of-two path goes through a
 // [T, E] fp32 workspace (:774-777); here every E <= 64 * 64 stays in registers.
 #include <algorithm>
 #include <type_traits>
@@ -42,7 +43,7 @@ struct ScoreIn<BF16> {
   }
 };
 
-// Cross-lane steps without LDS round trips: DPP inside each 16-lane row (row_ror:8,
+// Cross-lane reductions without LDS round trips: DPP inside each 16-lane row (row_ror:8,
 // row_ror:4, then quad xor 2 and xor 1), then v_permlane16_swap / v_permlane32_swap across
 // rows.  permlane{16,32}_swap(v, v) returns the lane's own row value and its partner row's
 // value (in row order), so combining the pair with a commutative operation gives every lane
@@ -65,48 +66,16 @@ __device__ __forceinline__ float dpp(float v) {
 // The two values of a row pair (16-lane rows 2r, 2r+1) or half pair (lanes 0-31, 32-63).
 struct Pair {
   float v0, v1;
-  int i0, i1;
 };
-__device__ __forceinline__ Pair swap16(float v, int i) {
-  const auto sv = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v),
-                                                   __builtin_bit_cast(int, v), false, false);
-  const auto si = __builtin_amdgcn_permlane16_swap(i, i, false, false);
-  return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1]),
-          (int)si[0], (int)si[1]};
+__device__ __forceinline__ Pair swap16(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  const auto sv = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1])};
 }
-__device__ __forceinline__ Pair swap32(float v, int i) {
-  const auto sv = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v),
-                                                   __builtin_bit_cast(int, v), false, false);
-  const auto si = __builtin_amdgcn_permlane32_swap(i, i, false, false);
-  return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1]),
-          (int)si[0], (int)si[1]};
-}
-
-// (value, index) order: the larger value wins, equal values go to the lower index.
-__device__ __forceinline__ void take_better(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
-}
-template <int CTRL>
-__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
-  take_better(v, i, dpp<CTRL>(v), dpp<CTRL>(i));
-}
-
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-  argmax_dpp<kDppRor8>(v, i);
-  argmax_dpp<kDppRor4>(v, i);
-  argmax_dpp<kDppXor2>(v, i);
-  argmax_dpp<kDppXor1>(v, i);
-  Pair p = swap16(v, i);
-  v = p.v0;
-  i = p.i0;
-  take_better(v, i, p.v1, p.i1);
-  p = swap32(v, i);
-  v = p.v0;
-  i = p.i0;
-  take_better(v, i, p.v1, p.i1);
+__device__ __forceinline__ Pair swap32(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  const auto sv = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1])};
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -114,9 +83,9 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kDppRor4>(v));
   v = fmaxf(v, dpp<kDppXor2>(v));
   v = fmaxf(v, dpp<kDppXor1>(v));
-  Pair p = swap16(v, 0);
+  Pair p = swap16(v);
   v = fmaxf(p.v0, p.v1);
-  p = swap32(v, 0);
+  p = swap32(v);
   return fmaxf(p.v0, p.v1);
 }
 
@@ -125,9 +94,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   v = v + dpp<kDppRor4>(v);
   v = v + dpp<kDppXor2>(v);
   v = v + dpp<kDppXor1>(v);
-  Pair p = swap16(v, 0);
+  Pair p = swap16(v);
   v = p.v0 + p.v1;
-  p = swap32(v, 0);
+  p = swap32(v);
   return p.v0 + p.v1;
 }
 
@@ -135,6 +104,91 @@ constexpr int kSoftmax = 0;  // topk_gating scoring
 constexpr int kScoreNone = 0;  // grouped_topk scoring_func 0: the scores as given
 constexpr int kSigmoid = 1;
 constexpr int kWavesPerBlock = 4;
+
+// Order-preserving key of a float (a larger float gives a larger unsigned key; -0 and +0 share
+// one key, as they compare equal).
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// One wave's chosen experts, in expert order, before ranking.
+struct ChosenList {
+  uint32_t key[kMaxK];
+  int idx[kMaxK];
+  float w[kMaxK];
+};
+
+// Chooses the k largest keys among the live slots of the wave (slot j of lane l is expert
+// l + 64*j; equal keys go to the lower expert) without k dependent argmax rounds:
+//  1. a threshold tau with at least k live keys >= tau and fewer than k above it, found bit
+//     by bit from the top (each step one compare per slot and a ballot count; the search
+//     stops once exactly k keys are >= tau);
+//  2. every key above tau, then the lowest-expert keys equal to tau until k are chosen;
+//  3. the chosen (key, expert, w) are compacted into `out` in expert order.
+// Returns the sum of the chosen w, the same on every lane.
+template <int VPL>
+__device__ __forceinline__ float choose_topk(const uint32_t (&key)[VPL], const float (&w)[VPL],
+                                             uint64_t live, int k, int lane, ChosenList& out) {
+  uint32_t tau = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) cnt += __popcll(__ballot(((live >> j) & 1) && key[j] >= cand));
+    if (cnt >= k) {
+      tau = cand;
+      if (cnt == k) break;  // exactly k keys >= tau: a larger tau would choose the same set
+    }
+  }
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) above += __popcll(__ballot(((live >> j) & 1) && key[j] > tau));
+  const int need = k - above;  // keys equal to tau still to take, lowest experts first
+  int eq_before = 0;
+  int base = 0;
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const bool lv = (live >> j) & 1;
+    const uint64_t eq = __ballot(lv && key[j] == tau);
+    const bool take = lv && (key[j] > tau || (key[j] == tau && eq_before + lanes_below(eq) < need));
+    eq_before += __popcll(eq);
+    const uint64_t tm = __ballot(take);
+    if (take) {
+      const int pos = base + lanes_below(tm);
+      out.key[pos] = key[j];
+      out.idx[pos] = lane + 64 * j;
+      out.w[pos] = w[j];
+      sum += w[j];
+    }
+    base += __popcll(tm);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return wave_sum(sum);
+}
+
+// Calls store(rank, expert, w) for each of the k chosen entries, rank = its place in
+// descending key order (ties: the lower expert, which is the earlier list entry).
+template <class F>
+__device__ __forceinline__ void emit_ranked(const ChosenList& c, int k, int lane, F&& store) {
+  for (int r = lane; r < k; r += 64) {
+    const uint32_t kr = c.key[r];
+    int rank = 0;
+    for (int q = 0; q < k; ++q) {
+      const uint32_t kq = c.key[q];
+      rank += (kq > kr || (kq == kr && q < r)) ? 1 : 0;
+    }
+    store(rank, c.idx[r], c.w[r]);
+  }
+}
 
 // VPL: experts per lane (E <= 64 * VPL).  OT: id output type (int32_t, uint32_t, int64_t).
 template <class IT, int VPL, int SF, class OT>
@@ -148,7 +202,6 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void topk_gating_kernel(
   const typename ScoreIn<IT>::raw* row = gating + t * num_experts;
 
   float score[VPL];
-  float choice[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int e = lane + 64 * j;
@@ -175,69 +228,26 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void topk_gating_kernel(
     for (int j = 0; j < VPL; ++j) score[j] = 1.0f / (1.0f + expf(-score[j]));
   }
 
-  uint64_t live = 0;  // bit j: expert lane + 64*j exists and is not chosen yet
+  uint64_t live = 0;  // bit j: expert lane + 64*j exists
+  uint32_t key[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int e = lane + 64 * j;
-    if (e < num_experts) {
-      live |= 1ull << j;
-      choice[j] = bias ? score[j] + bias[e] : score[j];
-    } else {
-      choice[j] = -INFINITY;
-    }
+    if (e < num_experts) live |= 1ull << j;
+    key[j] = order_key(e < num_experts && bias ? score[j] + bias[e] : score[j]);
   }
-
+  __shared__ ChosenList chosen[kWavesPerBlock];
+  ChosenList& c = chosen[threadIdx.x >> 6];
+  const float sum = choose_topk<VPL>(key, score, live, k, lane, c);
+  const float denom = renormalize ? (sum > 0.0f ? sum : 1.0f) : 1.0f;
   float* wrow = weights + t * k;
   OT* irow = ids + t * k;
   int* srow = token_expert_indices + t * k;
-  float sum = 0.0f;
-  float kept[kMaxK / 64];  // lane l keeps the weight of round 64*s + l in kept[s]
-#pragma unroll
-  for (int s = 0; s < kMaxK / 64; ++s) kept[s] = 0.0f;
-  for (int r = 0; r < k; ++r) {
-    // lane-local argmax over its live experts in ascending expert order; the first live
-    // slot is taken even when its choice is -inf, so such an expert still wins over an
-    // absent one
-    float bv = -INFINITY;
-    int bi = num_experts;
-    float bw = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      if (((live >> j) & 1) && (choice[j] > bv || bi == num_experts)) {
-        bv = choice[j];
-        bi = lane + 64 * j;
-        bw = score[j];
-      }
-    }
-    float wv = bv;
-    int wi = bi;
-    wave_argmax(wv, wi);
-    // the winner's unbiased score comes from the lane that owns it (wi is wave-uniform)
-    wi = __builtin_amdgcn_readfirstlane(wi);
-    const float w = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bw), wi & 63));
-    if ((wi & 63) == lane) {
-#pragma unroll
-      for (int j = 0; j < VPL; ++j)
-        if (j == (wi >> 6)) live &= ~(1ull << j);
-    }
-    sum += w;
-    if (lane == (r & 63)) {
-#pragma unroll
-      for (int s = 0; s < kMaxK / 64; ++s)
-        if (s == (r >> 6)) kept[s] = w;
-    }
-    if (lane == 0) {
-      irow[r] = (OT)wi;
-      srow[r] = (int)((int64_t)r * num_tokens + t);
-    }
-  }
-  const float denom = renormalize ? (sum > 0.0f ? sum : 1.0f) : 1.0f;
-#pragma unroll
-  for (int s = 0; s < kMaxK / 64; ++s) {
-    const int r = 64 * s + lane;
-    if (r < k) wrow[r] = renormalize ? kept[s] / denom : kept[s];
-  }
+  emit_ranked(c, k, lane, [&](int rank, int e, float w) {
+    irow[rank] = (OT)e;
+    wrow[rank] = renormalize ? w / denom : w;
+  });
+  for (int r = lane; r < k; r += 64) srow[r] = (int)((int64_t)r * num_tokens + t);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -332,42 +342,22 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void grouped_topk_kernel(
     return;
   }
 
-  uint64_t live = 0;
+  uint64_t live = 0;  // bit j: expert lane + 64*j exists and sits in a kept group
+  uint32_t key[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int e = lane + 64 * j;
     if (e < num_experts && ((kept >> (e / epg)) & 1)) live |= 1ull << j;
+    key[j] = order_key(choice[j]);
   }
-  float sum = 0.0f;
-  float kept_w = 0.0f;  // lane r keeps the unbiased score of round r (k <= 64)
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int bi = 1 << 30;
-    float bw = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      if (((live >> j) & 1) && (choice[j] > bv || bi == (1 << 30))) {
-        bv = choice[j];
-        bi = lane + 64 * j;
-        bw = score[j];
-      }
-    }
-    wave_argmax(bv, bi);
-    const int wi = __builtin_amdgcn_readfirstlane(bi);
-    const float w = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bw), wi & 63));
-    if ((wi & 63) == lane) {
-#pragma unroll
-      for (int j = 0; j < VPL; ++j)
-        if (j == (wi >> 6)) live &= ~(1ull << j);
-    }
-    sum += w;
-    if (lane == r) kept_w = w;
-    if (lane == 0) irow[r] = wi;
-  }
+  __shared__ ChosenList chosen[kWavesPerBlock];
+  const float sum = choose_topk<VPL>(key, score, live, k, lane, chosen[wave]);
   const float scale =
       renormalize ? routed_scaling_factor / (1e-20f + sum) : routed_scaling_factor;
-  if (lane < k) vrow[lane] = kept_w * scale;
+  emit_ranked(chosen[wave], k, lane, [&](int rank, int e, float w) {
+    irow[rank] = e;
+    vrow[rank] = w * scale;
+  });
 }
 
 template <class IT, class BT, int SF>
