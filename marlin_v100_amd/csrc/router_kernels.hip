@@ -78,6 +78,18 @@ __device__ __forceinline__ Pair swap32(float v) {
   return {__builtin_bit_cast(float, (int)sv[0]), __builtin_bit_cast(float, (int)sv[1])};
 }
 
+// Merges two (largest, second largest) pairs of a multiset: a repeated maximum counts twice.
+__device__ __forceinline__ void top2_merge(float a1, float b1, float a2, float b2, float& m1,
+                                           float& m2) {
+  m1 = fmaxf(a1, b1);
+  m2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+}
+template <int CTRL>
+__device__ __forceinline__ void top2_dpp(float& m1, float& m2) {
+  const float o1 = dpp<CTRL>(m1), o2 = dpp<CTRL>(m2);
+  top2_merge(m1, o1, m2, o2, m1, m2);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kDppRor8>(v));
   v = fmaxf(v, dpp<kDppRor4>(v));
@@ -260,8 +272,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void topk_gating_kernel(
 // the row falls back to experts 0..k-1 with weight 1/k (:587-600).  Inputs that are not
 // finite do not compete (their choice is -inf, :623-628).
 // Scores are computed in fp32 (the reference test oracle's arithmetic,
-// tests/test_marlin_moe.py:136-191).  Choice values pass through LDS so that lane g can take
-// the top two of group g.
+// tests/test_marlin_moe.py:136-191).  Groups of 16, 32 or 64 experts take their top two by
+// cross-lane steps; other sizes pass the choices through LDS so that lane g scans group g.
 // ---------------------------------------------------------------------------------------
 template <class BT>
 __device__ __forceinline__ float load_bias(const void* b, int e) {
@@ -292,35 +304,63 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void grouped_topk_kernel(
     if constexpr (SF == kSigmoid) x = 1.0f / (1.0f + expf(-x));
     score[j] = x;
     choice[j] = finite ? x + load_bias<BT>(bias, e) : -INFINITY;
-    if (e < num_experts) choice_lds[wave][e] = choice[j];
+  }
+
+  // group scores (the sum of each group's two largest choices) into gscore_lds[wave][g]
+  __shared__ float gscore_lds[kWavesPerBlock][32];
+  if (epg == 16 || epg == 32 || epg == 64) {
+    // a group is one 16-lane row, a row pair or the whole wave of a slot: merge (largest,
+    // second largest) pairs with the cross-lane steps; the group's first lane writes it
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float m1 = choice[j], m2 = -INFINITY;
+      top2_dpp<kDppRor8>(m1, m2);
+      top2_dpp<kDppRor4>(m1, m2);
+      top2_dpp<kDppXor2>(m1, m2);
+      top2_dpp<kDppXor1>(m1, m2);
+      if (epg >= 32) {
+        const Pair a = swap16(m1), b = swap16(m2);
+        top2_merge(a.v0, a.v1, b.v0, b.v1, m1, m2);  // the rows' largest, then seconds
+      }
+      if (epg == 64) {
+        const Pair a = swap32(m1), b = swap32(m2);
+        top2_merge(a.v0, a.v1, b.v0, b.v1, m1, m2);  // the rows' largest, then seconds
+      }
+      const int e = lane + 64 * j;
+      if (e < num_experts && e % epg == 0) gscore_lds[wave][e / epg] = m1 + m2;
+    }
+  } else {
+    // other group sizes: lane g < n_group scans group g through LDS
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane + 64 * j;
+      if (e < num_experts) choice_lds[wave][e] = choice[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < n_group) {
+      float m1 = -INFINITY, m2 = -INFINITY;
+      const float* grp = &choice_lds[wave][lane * epg];
+      for (int i = 0; i < epg; ++i) {
+        const float v = grp[i];
+        if (v > m1) {
+          m2 = m1;
+          m1 = v;
+        } else if (v > m2) {
+          m2 = v;
+        }
+      }
+      gscore_lds[wave][lane] = epg >= 2 ? m1 + m2 : m1;
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float gscore = lane < n_group ? gscore_lds[wave][lane] : -INFINITY;
 
-  // group scores: lane g < n_group sums the two largest choices of group g
-  float gscore = -INFINITY;
-  if (lane < n_group) {
-    float m1 = -INFINITY, m2 = -INFINITY;
-    const float* grp = &choice_lds[wave][lane * epg];
-    for (int i = 0; i < epg; ++i) {
-      const float v = grp[i];
-      if (v > m1) {
-        m2 = m1;
-        m1 = v;
-      } else if (v > m2) {
-        m2 = v;
-      }
-    }
-    gscore = epg >= 2 ? m1 + m2 : m1;
-  }
   // keep the topk_group best groups: lane g counts the groups that beat it (a larger score,
   // or an equal score and a lower index) and is kept when fewer than topk_group do
-  __shared__ float gscore_lds[kWavesPerBlock][32];
-  if (lane < n_group) gscore_lds[wave][lane] = gscore;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   int rank = 64;
   if (lane < n_group) {
     rank = 0;

@@ -166,6 +166,7 @@ GROUPED = [  # (T, E, n_group, topk_group, topk)
     (16, 256, 8, 4, 8),      # DeepSeek-V3 shape
     (33, 64, 8, 3, 6), (7, 96, 4, 2, 5), (5, 160, 32, 4, 4), (9, 1024, 16, 4, 32),
     (4, 512, 1, 1, 22), (3, 8, 8, 8, 8), (2048, 256, 8, 4, 8),
+    (6, 128, 8, 2, 6), (5, 512, 32, 8, 16),  # 16 experts per group
 ]
 
 
@@ -222,6 +223,11 @@ def test_grouped_topk_fallback_and_errors():
     vals, ids = capi.grouped_topk(scores, 4, 2, 4, True, 1.0, torch.zeros(16, device="cuda"), 1)
     assert ids.cpu().tolist() == [[0, 1, 2, 3]] * 3
     np.testing.assert_allclose(vals.cpu().numpy(), 0.25)
+    # the same with 16 experts per group (group scores by cross-lane steps)
+    scores = torch.full((2, 64), float("nan"), device="cuda")
+    vals, ids = capi.grouped_topk(scores, 4, 2, 3, False, 1.0, torch.zeros(64, device="cuda"), 0)
+    assert ids.cpu().tolist() == [[0, 1, 2]] * 2
+    np.testing.assert_allclose(vals.cpu().numpy(), 1.0 / 3.0, rtol=1e-6)
     from marlin_v100_amd import _custom_ops as ops
     with pytest.raises(RuntimeError, match="num_experts should be divisible by n_group"):
         ops.grouped_topk(torch.randn((2, 10), device="cuda"), 4, 2, 2, True, 1.0,
