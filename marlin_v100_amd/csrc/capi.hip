@@ -228,6 +228,10 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // with no more 16-column groups than CUs, 16-column groups keep every CU streaming
     // (cfg1 4096x4096: 6.1 us against 6.8 us with 32-column groups on half the CUs)
     if (int_operand && N % 16 == 0 && N / 16 <= cus) nt = 1, depth = 4, occ = 1;
+    // a single row needs few activation registers: two steps in flight at three waves per
+    // SIMD stream a little faster there (cfg2 M=1: 19.0 against 19.4-19.6 us; at M=16 the
+    // third step wins)
+    if (M == 1 && nt == 4 && depth == 3 && occ == 3) depth = 2;
     if (const char* t = getenv("MARLIN_MI355X_DECODE")) {
       sscanf(t, "%d,%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit, &occ);
     } else if (occ == 3) {
