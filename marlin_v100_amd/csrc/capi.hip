@@ -232,6 +232,9 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // SIMD stream a little faster there (cfg2 M=1: 19.0 against 19.4-19.6 us; at M=16 the
     // third step wins)
     if (M == 1 && nt == 4 && depth == 3 && occ == 3) depth = 2;
+    // MXFP4 from four rows on: 64-column groups (cfg4 shape, M = 4 / 8 / 16: 9.1 / 9.0 / 9.6
+    // against 9.9 / 10.0 / 10.4 us with 32-column groups; NVFP4 keeps 32 columns at every M)
+    if (kinds.fmt == FMT_MXFP4 && M >= 4) nt = 4;
     if (const char* t = getenv("MARLIN_MI355X_DECODE")) {
       sscanf(t, "%d,%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit, &occ);
     } else if (occ == 3) {
