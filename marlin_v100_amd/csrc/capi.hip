@@ -228,10 +228,10 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // with no more 16-column groups than CUs, 16-column groups keep every CU streaming
     // (cfg1 4096x4096: 6.1 us against 6.8 us with 32-column groups on half the CUs)
     if (int_operand && N % 16 == 0 && N / 16 <= cus) nt = 1, depth = 4, occ = 1;
-    // a single row needs few activation registers: two steps in flight at three waves per
-    // SIMD stream a little faster there (cfg2 M=1: 19.0 against 19.4-19.6 us; at M=16 the
-    // third step wins)
-    if (M == 1 && nt == 4 && depth == 3 && occ == 3) depth = 2;
+    // up to eight rows, two steps in flight at three waves per SIMD stream a little faster
+    // (cfg2 shape, M = 1 / 2 / 4 / 8: 18.9 / 19.1 / 19.4 / 19.9 against 19.3 / 19.5 / 19.9 /
+    // 20.5 us with three; level at M = 16)
+    if (M <= 8 && nt == 4 && depth == 3 && occ == 3) depth = 2;
     // MXFP4 from four rows on: 64-column groups (cfg4 shape, M = 4 / 8 / 16: 9.1 / 9.0 / 9.6
     // against 9.9 / 10.0 / 10.4 us with 32-column groups; NVFP4 keeps 32 columns at every M)
     if (kinds.fmt == FMT_MXFP4 && M >= 4) nt = 4;
