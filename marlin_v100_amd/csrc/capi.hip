@@ -316,10 +316,12 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= env_int("MARLIN_MI355X_SMALL_GROUP_MAX_M", 1024))
       bm = 32;
     int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
-    // per-weight dequant (fp4, small groups) in 32-row blocks up to M = 64: 128-column tiles
-    // with at most two K splits (cfg4 M=64: MXFP4 27.3 / NVFP4 28.6 us against 35.0 / 36.6
-    // with 256-column tiles and the occupancy-derived split; M = 512 keeps 256 columns)
-    const bool small_group_narrow = kinds.gsm == GSM_SMALL && bm == 32 && M <= 64 && N % 128 == 0;
+    // fp4 weights in 32-row blocks up to M = 64: 128-column tiles with at most two K splits
+    // (cfg4 M=64: MXFP4 27.3 / NVFP4 28.6 us against 35.0 / 36.6 with 256-column tiles and
+    // the occupancy-derived split; M = 512 keeps 256 columns; integer weights with small
+    // groups are not measured here and keep the general rule)
+    const bool small_group_narrow = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) &&
+                                    bm == 32 && M <= 64 && N % 128 == 0;
     if (small_group_narrow) nt = 2;
     if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
     nt = env_int("MARLIN_MI355X_STREAM_NT", nt);
