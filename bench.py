@@ -3,7 +3,10 @@
 Headline (`value`): weight GB/s of marlin_gemm on BASELINE configs[1] -- AWQ-style uint4 +
 float zero point, group 128, bf16 activations, K=5120, N=34816 -- at M=16 (decode).  One
 "step" is one marlin_gemm call on that workload with all inputs resident in HBM.  Weight
-copies rotate through >= 512 MiB so the 256 MB Infinity Cache cannot hold them.
+copies rotate through >= 512 MiB so the 256 MB Infinity Cache cannot hold them.  Calls
+shorter than 60 us are timed from a captured HIP graph of the rotating calls (host dispatch
+would otherwise set the pace); longer ones eagerly.  Both time with HIP events on the
+stream the kernels run on.
 
 The same JSON line carries every other BASELINE configuration (`configs`): cfg1 u4b8 fp16,
 cfg2 at M in {1,16,128,1024}, cfg3 u8b128 M=4096 (MFMA bound), cfg4 MXFP4/NVFP4 at
@@ -167,6 +170,43 @@ def time_calls(fn_list, steps, warmup):
     return start.elapsed_time(end) / 1e3 / steps
 
 
+def time_graph(fn_list, steps, warmup, per_graph=None):
+    """Average per-call device time with the host out of the loop: the rotating calls are
+    captured into one HIP graph on a side stream (after an eager warm-up of every call on
+    that stream, so no workspace is sized inside the capture) and the graph is replayed;
+    HIP events are recorded on that same stream.  Returns (seconds per call, calls)."""
+    import torch
+
+    n = len(fn_list)
+    per_graph = per_graph or n * max(1, -(-50 // n))  # whole rotations, >= 50 calls
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(max(warmup, n)):
+            fn_list[i % n]()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(per_graph):
+                fn_list[i % n]()
+        replays = max(2, -(-steps // per_graph))
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(side)
+        for _ in range(replays):
+            graph.replay()
+        end.record(side)
+        torch.cuda.synchronize()
+    torch.cuda.current_stream().wait_stream(side)
+    return start.elapsed_time(end) / 1e3 / (replays * per_graph), replays * per_graph
+
+
+# calls shorter than this are timed from a captured graph (host dispatch would set the pace)
+GRAPH_BELOW_US = 60.0
+
+
 def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
     import torch
 
@@ -179,7 +219,9 @@ def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
     gen = torch.Generator(device="cuda").manual_seed(seed)
     first = make_weights(fmt, k, n, dtype, gen)
     wbytes = meta_bytes(first)
-    copies = max(1, min(8, -(-ROTATE_BYTES // wbytes)))
+    # distinct weight copies rotated through >= 512 MiB (twice the 256 MB Infinity Cache), so
+    # every call streams its weights from HBM
+    copies = max(1, -(-ROTATE_BYTES // wbytes))
     weights = [first] + [make_weights(fmt, k, n, dtype, gen) for _ in range(copies - 1)]
     a = torch.randn((m, k), generator=gen, device="cuda").to(dtype)
     c = torch.empty((m, n), device="cuda", dtype=dtype)
@@ -193,6 +235,10 @@ def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
 
     fns = [call(wt) for wt in weights]
     t = time_calls(fns, steps, warmup)
+    timing = "eager"
+    if t * 1e6 < GRAPH_BELOW_US:
+        t, _ = time_graph(fns, steps, warmup)
+        timing = "graph"
     alg_bytes = wbytes + a.numel() * 2 + c.numel() * 2
     flops = 2.0 * m * n * k
     gbs = alg_bytes / t / 1e9
@@ -204,6 +250,7 @@ def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
         "alg_GBs": round(gbs, 1), "TFLOPs": round(tflops, 2), "bound": bound,
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
         "alg_bytes": alg_bytes, "weight_bytes": wbytes, "flops": flops, "rotated_copies": copies,
+        "rotated_bytes": copies * wbytes, "timing": timing,
     }
 
 
@@ -275,19 +322,7 @@ def router_case(key, tokens, steps, warmup, seed, grouped=False):
     # eager calls are bound by host dispatch (torch op -> C ABI -> launch); the device rate
     # comes from a captured graph of 50 back-to-back calls (the kernel writes no memset node)
     t_eager = time_calls([fn], steps, warmup)
-    per_graph = 50
-    graph = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        fn()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            for _ in range(per_graph):
-                fn()
-    torch.cuda.current_stream().wait_stream(side)
-    replays = max(2, steps // per_graph)
-    t = time_calls([graph.replay], replays, 2) / per_graph
+    t, _ = time_graph([fn], steps, warmup, per_graph=50)
     alg_bytes = tokens * E * 4 + tokens * topk * 12
     return {"key": key, "T": tokens, "E": E, "topk": topk, "us": round(t * 1e6, 2),
             "us_eager_dispatch": round(t_eager * 1e6, 2), "alg_bytes": alg_bytes,
@@ -299,13 +334,27 @@ def router_case(key, tokens, steps, warmup, seed, grouped=False):
 # CPU reference path (bounded sample), timed on the host cores
 # ---------------------------------------------------------------------------------------
 
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the CPUs this process may run on, capped by
+    OMP_NUM_THREADS when the job sets it (the GPU box grants each job a CPU share and sets
+    OMP_NUM_THREADS to it)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
 def cpu_baseline(m, k, n):
+    """The reference's CPU path on the headline workload: dequantize (the oracle's
+    restatement of the reference dequant) then fp32 torch.matmul (tests/helpers.py:1749-1760),
+    each timed separately, median of 5 after one warm-up, on a bounded column slice."""
     import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle as O
 
-    cores = min(16, os.cpu_count() or 1)
+    cores = cpu_threads()
     torch.set_num_threads(cores)
     gen = torch.Generator().manual_seed(1001)
     # bounded sample: the full K, a 4096-column slice of N (weights dominate the work)
@@ -314,25 +363,32 @@ def cpu_baseline(m, k, n):
     q, s, _z, zp = O.quantize_with_zero_point(w, 128, 4, torch.bfloat16)
     a = torch.randn((m, k), generator=gen).bfloat16()
 
-    def run():
-        deq = O.dequant_int(q, s, "u4", torch.bfloat16, zp)
-        return O.gemm_ref(a, deq)
+    def dequant():
+        return O.dequant_int(q, s, "u4", torch.bfloat16, zp)
 
-    run()
-    times = []
+    deq = dequant()
+    O.gemm_ref(a, deq)
+    t_deq, t_mm = [], []
     t_end = time.time() + 20.0
-    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+    while len(t_deq) < 5 or (time.time() < t_end and len(t_deq) < 25):
         t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    t = times[len(times) // 2]
+        deq = dequant()
+        t1 = time.perf_counter()
+        O.gemm_ref(a, deq)
+        t2 = time.perf_counter()
+        t_deq.append(t1 - t0)
+        t_mm.append(t2 - t1)
+    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+    td, tm = med(t_deq), med(t_mm)
+    t = td + tm
     wbytes = k * ns // 2 + 2 * (k // 128) * ns * 2
     return {"value": round(wbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores,
             "kind": "port",
             "sample": f"oracle dequant (uint4+zp g128 -> bf16) + fp32 torch.matmul, "
-                      f"M={m} K={k} N={ns} (column slice of N={n}), median of {len(times)} runs",
-            "ms_per_call": round(t * 1e3, 2)}
+                      f"M={m} K={k} N={ns} (column slice of N={n}), median of {len(t_deq)} runs "
+                      f"after one warm-up, {cores} threads",
+            "ms_per_call": round(t * 1e3, 2), "dequant_ms": round(td * 1e3, 2),
+            "matmul_ms": round(tm * 1e3, 2)}
 
 
 def main() -> int:

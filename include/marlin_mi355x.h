@@ -185,7 +185,11 @@ marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_
                                   void* out, marlin_stream_t stream);
 
 /*
- * Top-k reduction of MoE route outputs: out[t, :] = sum_k input[t, k, :].
+ * Top-k reduction of MoE route outputs: out[t, :] = sum_k input[t, k, :], input
+ * [num_tokens, top_k, hidden] and out [num_tokens, hidden] contiguous, fp16, bf16 or fp32.
+ * For 16-bit types and top_k 2..4 every addition rounds to the element type (the
+ * reference's kernel); otherwise the sum is accumulated in fp32 and rounded once (the
+ * reference's at::sum_out).  No limit on num_tokens.
  * Replaces torch.ops._moe_C.moe_sum (reference csrc/moe/moe_align_sum_kernels.cu:598-639).
  */
 marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t num_tokens,

@@ -35,18 +35,13 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-HIP_SOURCES = [
+# (the GEMM instance files take longest: they go to the compile pool first)
+HIP_SOURCES = [f"gemm_{fmt}_{at}.hip" for fmt in ("u4", "u4b8", "u8", "u8b128", "fp8", "mxfp4",
+                                                  "nvfp4") for at in ("bf16", "f16")] + [
     "capi.hip",
     "repack.hip",
     "aux_kernels.hip",
     "router_kernels.hip",
-    "gemm_u4b8.hip",
-    "gemm_u4.hip",
-    "gemm_u8b128.hip",
-    "gemm_u8.hip",
-    "gemm_fp8.hip",
-    "gemm_mxfp4.hip",
-    "gemm_nvfp4.hip",
 ]
 
 LIB_NAME = "libmarlin_mi355x.so"
@@ -59,16 +54,30 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
 
 
-def _compile_hip(src: str) -> str:
+def _stale(src: str, obj: str) -> bool:
+    """Object older than its source or any header in csrc/ or include/."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)]
+    deps += [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith(".h")]
+    inc = os.path.join(ROOT, "include")
+    deps += [os.path.join(inc, h) for h in os.listdir(inc) if h.endswith(".h")]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _compile_hip(src: str, incremental: bool = False) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if incremental and not _stale(src, obj):
+        return obj
     _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 
-def build_library(jobs: int) -> str:
+def build_library(jobs: int, incremental: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile_hip, HIP_SOURCES))
+        objs = list(ex.map(lambda src: _compile_hip(src, incremental), HIP_SOURCES))
     out = os.path.join(HERE, LIB_NAME)
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
@@ -119,11 +128,11 @@ def build_bindings() -> list[str]:
         return [f.result() for f in futs]
 
 
-def build(jobs: int | None = None, only_lib: bool = False) -> list[str]:
+def build(jobs: int | None = None, only_lib: bool = False, incremental: bool = False) -> list[str]:
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     jobs = jobs or min(8, os.cpu_count() or 4)
-    outs = [build_library(jobs)]
+    outs = [build_library(jobs, incremental)]
     if not only_lib:
         outs += build_bindings()
     return outs
@@ -133,8 +142,10 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--only-lib", action="store_true")
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only sources older than their object (development)")
     args = ap.parse_args()
-    for p in build(args.jobs, args.only_lib):
+    for p in build(args.jobs, args.only_lib, args.incremental):
         print("built", os.path.relpath(p, ROOT))
     return 0
 

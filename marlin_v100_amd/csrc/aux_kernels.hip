@@ -273,7 +273,8 @@ hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, i
 // moe_sum: out[t, h] = sum_k in[t, k, h] as the reference computes it
 // (moe_align_sum_kernels.cu:350-363, 597-639): for top-k 2..4 its kernel adds in the element
 // type, rounding after every addition; otherwise at::sum_out accumulates in fp32 and rounds
-// once.  `step_round` selects the former.
+// once.  `step_round` selects the former.  fp32 inputs add in fp32 either way (for top-k
+// beyond 4 in index order; at::sum_out's order is its own, so fp32 agrees to rounding).
 // ---------------------------------------------------------------------------------------
 template <class AT>
 __device__ __forceinline__ float moe_sum_add(float s, float x, bool step_round) {
@@ -281,17 +282,34 @@ __device__ __forceinline__ float moe_sum_add(float s, float x, bool step_round) 
   return step_round ? raw16_to_float(to_raw16(v, AT{}), AT{}) : v;
 }
 
+// One output element per thread, any hidden size and alignment; the flat index runs over
+// tokens x hidden, so the token count is not limited by a grid dimension.
 template <class AT>
 __global__ void moe_sum_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
                                int64_t tokens, int topk, int64_t hidden) {
-  const int64_t t = blockIdx.y;
   const bool step_round = topk >= 2 && topk <= 4;
-  for (int64_t h = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; h < hidden;
-       h += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t n = tokens * hidden;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / hidden;
+    const int64_t h = i - t * hidden;
     float s = 0.f;
     for (int k = 0; k < topk; ++k)
       s = moe_sum_add<AT>(s, raw16_to_float(in[(t * topk + k) * hidden + h], AT{}), step_round);
-    out[t * hidden + h] = to_raw16(s, AT{});
+    out[i] = to_raw16(s, AT{});
+  }
+}
+
+__global__ void moe_sum_kernel_f32(const float* __restrict__ in, float* __restrict__ out,
+                                   int64_t tokens, int topk, int64_t hidden) {
+  const int64_t n = tokens * hidden;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / hidden;
+    const int64_t h = i - t * hidden;
+    float s = 0.f;
+    for (int k = 0; k < topk; ++k) s += in[(t * topk + k) * hidden + h];
+    out[i] = s;
   }
 }
 
@@ -332,34 +350,40 @@ __global__ void moe_sum_kernel_v8(const uint16_t* __restrict__ in, uint16_t* __r
   }
 }
 
-hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, int64_t hidden,
+// kind: 0 fp16, 1 bf16, 2 fp32
+hipError_t launch_moe_sum(const void* in, int kind, int64_t tokens, int topk, int64_t hidden,
                           void* out, hipStream_t stream) {
   if (tokens == 0 || hidden == 0) return hipSuccess;
-  const uint16_t* i16v = reinterpret_cast<const uint16_t*>(in);
-  uint16_t* o16v = reinterpret_cast<uint16_t*>(out);
+  const int64_t total = tokens * hidden;
+  if (kind == 2) {
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 256 * 16);
+    hipLaunchKernelGGL(moe_sum_kernel_f32, dim3(blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const float*>(in), reinterpret_cast<float*>(out), tokens,
+                       topk, hidden);
+    return hipGetLastError();
+  }
+  const bool bf16 = kind == 1;
+  const uint16_t* i16 = reinterpret_cast<const uint16_t*>(in);
+  uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
   if (hidden % 8 == 0 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
       reinterpret_cast<uintptr_t>(out) % 16 == 0) {
     const int64_t n = tokens * (hidden / 8);
     const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 256 * 16);
     if (bf16)
-      hipLaunchKernelGGL((moe_sum_kernel_v8<BF16>), dim3(blocks), dim3(256), 0, stream, i16v,
-                         o16v, tokens, topk, hidden);
+      hipLaunchKernelGGL((moe_sum_kernel_v8<BF16>), dim3(blocks), dim3(256), 0, stream, i16, o16,
+                         tokens, topk, hidden);
     else
-      hipLaunchKernelGGL((moe_sum_kernel_v8<F16>), dim3(blocks), dim3(256), 0, stream, i16v,
-                         o16v, tokens, topk, hidden);
+      hipLaunchKernelGGL((moe_sum_kernel_v8<F16>), dim3(blocks), dim3(256), 0, stream, i16, o16,
+                         tokens, topk, hidden);
     return hipGetLastError();
   }
-  unsigned gx = (unsigned)((hidden + 255) / 256);
-  if (gx > 64) gx = 64;
-  dim3 grid(gx, (unsigned)tokens);
-  const uint16_t* i16 = reinterpret_cast<const uint16_t*>(in);
-  uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
+  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 256 * 16);
   if (bf16)
-    hipLaunchKernelGGL((moe_sum_kernel<BF16>), grid, dim3(256), 0, stream, i16, o16, tokens, topk,
-                       hidden);
+    hipLaunchKernelGGL((moe_sum_kernel<BF16>), dim3(blocks), dim3(256), 0, stream, i16, o16,
+                       tokens, topk, hidden);
   else
-    hipLaunchKernelGGL((moe_sum_kernel<F16>), grid, dim3(256), 0, stream, i16, o16, tokens, topk,
-                       hidden);
+    hipLaunchKernelGGL((moe_sum_kernel<F16>), dim3(blocks), dim3(256), 0, stream, i16, o16,
+                       tokens, topk, hidden);
   return hipGetLastError();
 }
 

@@ -11,6 +11,7 @@
 #include <sstream>
 #include <string>
 #include <tuple>
+#include <unordered_map>
 #include <utility>
 
 #include "../../include/marlin_mi355x.h"
@@ -123,12 +124,22 @@ struct Workspace {
 };
 
 // One zero-initialised workspace per (device, stream).  Kernels leave it zeroed, so it is
-// cleared only when allocated.  Growing it synchronises the stream (first calls only).
+// cleared only when allocated.  Growing it synchronises the stream (first calls only); a
+// stream that is capturing a graph cannot allocate, so growth there is an error that names
+// the remedy instead of an allocation and a memset recorded into the graph.
 Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t need_counters) {
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, Workspace> spaces;
   std::lock_guard<std::mutex> lk(mu);
   Workspace& w = spaces[{dev, stream}];
+  if (need_elems > w.ws_elems || need_counters > w.n_counters) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    check_hip(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
+    check_supported(cs == hipStreamCaptureStatusNone,
+                    "split-K workspace for this shape is not yet allocated on the capturing "
+                    "stream: run the same shape once on that stream before capturing, or use "
+                    "marlin_gemm_no_alloc");
+  }
   if (need_elems > w.ws_elems) {
     size_t n = std::max<size_t>(need_elems, std::max<size_t>(2 * w.ws_elems, size_t(1) << 20));
     if (w.ws) {
@@ -191,9 +202,72 @@ Fit kernel_fit(const GemmLaunch& l) {
 }
 int blocks_per_cu(const GemmLaunch& l) { return kernel_fit(l).blocks_per_cu; }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
+// Whether the library holds an instance for a launch configuration (occupancy query only).
+bool instantiated(const GemmLaunch& l) {
+  GemmLaunch q = l;
+  int occ = 0;
+  q.occupancy = &occ;
+  q.scratch = nullptr;
+  GemmParams dummy{};
+  return dispatch_gemm(q, dummy, nullptr) == hipSuccess;
+}
+
+// Tuning overrides (MARLIN_MI355X_*), read once per process: the hot path reads no
+// environment.  -1 / unset means "the selector decides".
+struct Overrides {
+  bool decode_set = false;
+  int decode[5] = {0, 0, 0, 0, 0};  // nt, depth, wpb, ksplit, occ
+  bool tile_set = false;
+  int tile[3] = {0, 0, 1};          // bm, nt, ch
+  int split_k = -1;
+  int stream = 1;
+  int stream_max_m = 1 << 30;
+  int small_group_max_m = 1024;
+  int stream_nt = -1;
+  int xcd_group_m = -1;
+  int moe_split_k = -1;
+  int moe_group_m = 4;
+  int moe_decode = 1;
+  int moe_depth = 3;
+  int moe_wpb = 1;
+  bool any = false;  // some override is set (plans are then checked for an instance)
+};
+
+const Overrides& overrides() {
+  static const Overrides o = [] {
+    Overrides r;
+    auto env = [&](const char* name) -> const char* {
+      const char* v = getenv(name);
+      if (v && *v) {
+        r.any = true;
+        return v;
+      }
+      return nullptr;
+    };
+    auto env_int = [&](const char* name, int& dst) {
+      if (const char* v = env(name)) dst = atoi(v);
+    };
+    if (const char* t = env("MARLIN_MI355X_DECODE")) {
+      r.decode_set = sscanf(t, "%d,%d,%d,%d,%d", &r.decode[0], &r.decode[1], &r.decode[2],
+                            &r.decode[3], &r.decode[4]) == 5;
+    }
+    if (const char* t = env("MARLIN_MI355X_TILE")) {
+      r.tile_set = sscanf(t, "%d,%d,%d", &r.tile[0], &r.tile[1], &r.tile[2]) >= 2;
+    }
+    env_int("MARLIN_MI355X_SPLIT_K", r.split_k);
+    env_int("MARLIN_MI355X_STREAM", r.stream);
+    env_int("MARLIN_MI355X_STREAM_MAX_M", r.stream_max_m);
+    env_int("MARLIN_MI355X_SMALL_GROUP_MAX_M", r.small_group_max_m);
+    env_int("MARLIN_MI355X_STREAM_NT", r.stream_nt);
+    env_int("MARLIN_MI355X_XCD_GROUP_M", r.xcd_group_m);
+    env_int("MARLIN_MI355X_MOE_SPLIT_K", r.moe_split_k);
+    env_int("MARLIN_MI355X_MOE_GROUP_M", r.moe_group_m);
+    env_int("MARLIN_MI355X_MOE_DECODE", r.moe_decode);
+    env_int("MARLIN_MI355X_MOE_DEPTH", r.moe_depth);
+    env_int("MARLIN_MI355X_MOE_WPB", r.moe_wpb);
+    return r;
+  }();
+  return o;
 }
 
 // Dense selector.
@@ -212,6 +286,7 @@ int env_int(const char* name, int dflt) {
 // MARLIN_MI355X_DECODE="nt,depth,wpb,ksplit,occ" (nt 0 disables the decode kernel),
 // MARLIN_MI355X_TILE="bm,nt,ch" and MARLIN_MI355X_SPLIT_K override the choice (tuning).
 Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& kinds) {
+  const Overrides& ov = overrides();
   Plan p{};
   // Integer and fp8 weights with channelwise or >= 128-deep groups multiply raw codes
   // (integer-operand path): 64-column groups, three steps in flight.  fp4 weights and small
@@ -228,21 +303,26 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // with no more 16-column groups than CUs, 16-column groups keep every CU streaming
     // (cfg1 4096x4096: 6.1 us against 6.8 us with 32-column groups on half the CUs)
     if (int_operand && N % 16 == 0 && N / 16 <= cus) nt = 1, depth = 4, occ = 1;
-    // up to eight rows, two steps in flight at three waves per SIMD stream a little faster
-    // (cfg2 shape, M = 1 / 2 / 4 / 8: 18.9 / 19.1 / 19.4 / 19.9 against 19.3 / 19.5 / 19.9 /
-    // 20.5 us with three; level at M = 16)
-    if (M <= 8 && nt == 4 && depth == 3 && occ == 3) depth = 2;
     // MXFP4 from four rows on: 64-column groups (cfg4 shape, M = 4 / 8 / 16: 9.1 / 9.0 / 9.6
     // against 9.9 / 10.0 / 10.4 us with 32-column groups; NVFP4 keeps 32 columns at every M)
     if (kinds.fmt == FMT_MXFP4 && M >= 4) nt = 4;
-    if (const char* t = getenv("MARLIN_MI355X_DECODE")) {
-      sscanf(t, "%d,%d,%d,%d,%d", &nt, &depth, &wpb, &ksplit, &occ);
+    if (ov.decode_set) {
+      nt = ov.decode[0], depth = ov.decode[1], wpb = ov.decode[2], ksplit = ov.decode[3],
+      occ = ov.decode[4];
     } else if (occ == 3) {
       // three waves per SIMD where the instance's registers fit that budget without
-      // spilling (checked once per instance); the compiler's choice otherwise
-      GemmLaunch q = kinds;
-      q.bm = 16, q.nt = nt, q.ch = 1, q.depth = depth, q.wpb = wpb, q.ksplit = true, q.occ = 3;
-      if (kernel_fit(q).spills) occ = 1;
+      // spilling (checked once per instance); the compiler's choice otherwise.  Up to eight
+      // rows, two steps in flight at three waves per SIMD stream a little faster (cfg2
+      // shape, M = 1 / 2 / 4 / 8: 18.9 / 19.1 / 19.4 / 19.9 against 19.3 / 19.5 / 19.9 /
+      // 20.5 us with three; level at M = 16).  A spilling depth-2 instance falls back to
+      // depth 3, whose one-wave-per-SIMD instance always exists.
+      auto spills = [&](int d) {
+        GemmLaunch q = kinds;
+        q.bm = 16, q.nt = nt, q.ch = 1, q.depth = d, q.wpb = wpb, q.ksplit = true, q.occ = 3;
+        return kernel_fit(q).spills;
+      };
+      if (M <= 8 && nt == 4 && depth == 3 && !spills(2)) depth = 2;
+      else if (spills(depth)) occ = 1;
     }
     if (nt > 0 && N % (16 * nt) == 0) {
       const int64_t groups = N / (16 * nt);
@@ -294,8 +374,8 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
         splits = (int)std::min<int64_t>(splits, budget);
         splits = std::max(splits, 1);
       }
-      if (const char* t = getenv("MARLIN_MI355X_SPLIT_K")) {
-        splits = atoi(t);
+      if (ov.split_k >= 0) {
+        splits = ov.split_k;
         main_blocks = 0;
       }
       splits = std::max(1, std::min(splits, std::max(steps, 1)));
@@ -308,12 +388,12 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
   }
   // The multistage kernel (all of K's operands three steps ahead): 16..64-row blocks up to
   // M = 128, 128-row blocks (one wave per SIMD, accumulators in AGPRs) beyond.
-  if (env_int("MARLIN_MI355X_STREAM", 1) != 0 && M <= env_int("MARLIN_MI355X_STREAM_MAX_M", 1 << 30)) {
+  if (ov.stream != 0 && M <= ov.stream_max_m) {
     int bm = M <= 16 ? 16 : (M <= 32 ? 32 : (M <= 128 ? 64 : 128));
     // per-32/16 group metadata for 48+ rows does not fit the register budget: 32-row blocks
     // up to M = 1024, the tiled kernel beyond (measured on cfg4 MXFP4: 35 / 75 / 252 us at
     // M = 64 / 512 / 2048 against 47 / 184 / 211 us tiled)
-    if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= env_int("MARLIN_MI355X_SMALL_GROUP_MAX_M", 1024))
+    if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= ov.small_group_max_m)
       bm = 32;
     int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
     // fp4 weights in 32-row blocks up to M = 64: 128-column tiles with at most two K splits
@@ -324,7 +404,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
                                     bm == 32 && M <= 64 && N % 128 == 0;
     if (small_group_narrow) nt = 2;
     if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
-    nt = env_int("MARLIN_MI355X_STREAM_NT", nt);
+    if (ov.stream_nt >= 0) nt = ov.stream_nt;
     const bool small_meta_fits = !(kinds.gsm == GSM_SMALL && bm >= 48);
     if (nt > 0 && N % (64 * nt) == 0 && small_meta_fits) {
       p.bm = bm;
@@ -333,7 +413,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       p.stream = 1;
       p.m_blocks = (int)((M + bm - 1) / bm);
       p.n_blocks = (int)(N / (64 * nt));
-      p.xcd_group_m = env_int("MARLIN_MI355X_XCD_GROUP_M", bm >= 64 ? 4 : 0);
+      p.xcd_group_m = ov.xcd_group_m >= 0 ? ov.xcd_group_m : (bm >= 64 ? 4 : 0);
       GemmLaunch q = kinds;
       q.bm = bm;
       q.nt = nt;
@@ -346,7 +426,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       if (base < resident && steps >= 8)
         splits = (int)std::min<int64_t>(resident / base, steps / 4);
       if (small_group_narrow) splits = std::min(splits, 2);
-      splits = env_int("MARLIN_MI355X_SPLIT_K", splits);
+      if (ov.split_k >= 0) splits = ov.split_k;
       splits = std::max(1, std::min(splits, std::max(steps, 1)));
       p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
       p.splits = steps == 0 ? 1 : (steps + p.steps_per_split - 1) / p.steps_per_split;
@@ -375,18 +455,15 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     p.nt = 1;
     p.ch = 2;
   }
-  if (const char* t = getenv("MARLIN_MI355X_TILE")) {
-    int bm = 0, nt = 0, ch = 1;
-    if (sscanf(t, "%d,%d,%d", &bm, &nt, &ch) >= 2) {
-      p.bm = bm;
-      p.nt = nt;
-      p.ch = ch;
-    }
+  if (ov.tile_set) {
+    p.bm = ov.tile[0];
+    p.nt = ov.tile[1];
+    p.ch = ov.tile[2];
   }
   p.m_blocks = (int)((M + p.bm - 1) / p.bm);
   p.n_blocks = (int)(N / (64 * p.nt));
   p.xcd_group_m = p.bm >= 64 ? 4 : 0;
-  p.xcd_group_m = env_int("MARLIN_MI355X_XCD_GROUP_M", p.xcd_group_m);
+  if (ov.xcd_group_m >= 0) p.xcd_group_m = ov.xcd_group_m;
   const int steps = (int)(K / (128 * p.ch));
   const int64_t base = (int64_t)p.m_blocks * p.n_blocks;
   const int64_t target = (p.bm <= 32) ? (int64_t)cus * 4 : (int64_t)cus;
@@ -396,7 +473,7 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     const int min_steps = (p.bm <= 32) ? 2 : 4;
     splits = std::max(1, std::min(splits, std::max(1, steps / min_steps)));
   }
-  splits = env_int("MARLIN_MI355X_SPLIT_K", splits);
+  if (ov.split_k >= 0) splits = ov.split_k;
   if (steps == 0) splits = 1;
   splits = std::max(1, std::min(splits, std::max(steps, 1)));
   p.steps_per_split = steps == 0 ? 0 : (steps + splits - 1) / splits;
@@ -406,15 +483,18 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
 }
 
 hipError_t dispatch_gemm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
+#define MMI_CASE_FMT(E, F) \
+  case E: return l.bf16 ? launch_gemm_##F##_bf16(l, p, s) : launch_gemm_##F##_f16(l, p, s);
   switch (l.fmt) {
-    case FMT_U4B8: return launch_gemm_u4b8(l, p, s);
-    case FMT_U4: return launch_gemm_u4(l, p, s);
-    case FMT_U8B128: return launch_gemm_u8b128(l, p, s);
-    case FMT_U8: return launch_gemm_u8(l, p, s);
-    case FMT_FP8: return launch_gemm_fp8(l, p, s);
-    case FMT_MXFP4: return launch_gemm_mxfp4(l, p, s);
-    case FMT_NVFP4: return launch_gemm_nvfp4(l, p, s);
+    MMI_CASE_FMT(FMT_U4B8, u4b8)
+    MMI_CASE_FMT(FMT_U4, u4)
+    MMI_CASE_FMT(FMT_U8B128, u8b128)
+    MMI_CASE_FMT(FMT_U8, u8)
+    MMI_CASE_FMT(FMT_FP8, fp8)
+    MMI_CASE_FMT(FMT_MXFP4, mxfp4)
+    MMI_CASE_FMT(FMT_NVFP4, nvfp4)
   }
+#undef MMI_CASE_FMT
   return hipErrorInvalidValue;
 }
 
@@ -507,6 +587,161 @@ MetaCheck check_weight_meta(int64_t b_type_id, marlin_dtype_t a_dtype,
   return mc;
 }
 
+// ---- dense plan cache ---------------------------------------------------------------------
+// The selector's choice for one (device, format, dtype, group mode, M, N, K): the plan and
+// the kernel instance it launches.  Computed once per key (the selector queries occupancy
+// and register spills on first use), so a repeated shape costs one hash lookup.
+struct DensePlan {
+  Plan plan;
+  GemmLaunch launch;
+};
+
+struct PlanKey {
+  int dev, fmt, bf16, gsm;
+  int64_t m, n, k;
+  bool operator==(const PlanKey& o) const {
+    return dev == o.dev && fmt == o.fmt && bf16 == o.bf16 && gsm == o.gsm && m == o.m &&
+           n == o.n && k == o.k;
+  }
+};
+struct PlanKeyHash {
+  size_t operator()(const PlanKey& x) const {
+    uint64_t h = 1469598103934665603ull;
+    for (int64_t v : {(int64_t)x.dev, (int64_t)x.fmt, (int64_t)x.bf16, (int64_t)x.gsm, x.m, x.n, x.k})
+      h = (h ^ (uint64_t)v) * 1099511628211ull;
+    return (size_t)h;
+  }
+};
+
+const char* fmt_name(int fmt) {
+  static const char* names[] = {"uint4b8", "uint4", "uint8b128", "uint8", "fp8_e4m3", "mxfp4", "nvfp4"};
+  return (fmt >= 0 && fmt < 7) ? names[fmt] : "?";
+}
+
+DensePlan dense_plan(int dev, int fmt, bool bf16, int gsm, int64_t M, int64_t N, int64_t K) {
+  static std::mutex mu;
+  static std::unordered_map<PlanKey, DensePlan, PlanKeyHash> cache;
+  const PlanKey key{dev, fmt, (int)bf16, gsm, M, N, K};
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  GemmLaunch l{};
+  l.fmt = fmt;
+  l.bf16 = bf16;
+  l.gsm = gsm;
+  DensePlan d{};
+  d.plan = select_dense(M, N, K, device_cu_count(dev), l);
+  l.bm = d.plan.bm;
+  l.nt = d.plan.nt;
+  l.ch = d.plan.ch;
+  l.depth = d.plan.depth;
+  l.wpb = d.plan.wpb;
+  l.ksplit = d.plan.ksplit != 0;
+  l.occ = d.plan.occ;
+  l.stream = d.plan.stream != 0;
+  l.moe = false;
+  l.grid = (unsigned)d.plan.grid;
+  d.launch = l;
+  if (!instantiated(l)) {
+    std::ostringstream os;
+    os << "no " << fmt_name(fmt) << (bf16 ? "/bf16" : "/fp16") << " kernel instance for the "
+       << "selected configuration (bm " << l.bm << ", nt " << l.nt << ", ch " << l.ch
+       << ", depth " << l.depth << ", wpb " << l.wpb << ", ksplit " << l.ksplit << ", occ "
+       << l.occ << ", stream " << l.stream << ")";
+    if (overrides().any) os << "; a MARLIN_MI355X_* tuning override selects a configuration "
+                               "this build does not instantiate";
+    check_supported(false, os.str());
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (cache.size() >= (1u << 16)) cache.clear();  // bound the cache for callers with many shapes
+  cache.emplace(key, d);
+  return d;
+}
+
+// A validated dense call: its plan, the kernel parameters (all but the split-K scratch)
+// and the scratch it needs.
+struct DenseCall {
+  bool empty;  // nothing to compute (M = 0 or N = 0)
+  int dev;
+  DensePlan plan;
+  GemmParams params;
+  size_t ws_elems;     // fp32 partial sums (splits > 1)
+  size_t ws_counters;  // arrival counters (splits > 1)
+};
+
+// Validation of marlin_gemm (reference marlin.cu:83-506) and everything the launch needs
+// except the split-K scratch.
+DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_stride, void* c,
+                      const int32_t* b_q_weight, int64_t b_q_weight_numel, const void* b_bias,
+                      int64_t b_bias_numel, const void* b_scales, marlin_dtype_t b_scales_dtype,
+                      int64_t b_scales_numel, int64_t num_groups, int64_t a_scales_numel,
+                      const float* global_scale, int64_t global_scale_numel, const void* b_zeros,
+                      marlin_dtype_t b_zeros_dtype, int64_t b_zeros_numel, int64_t g_idx_numel,
+                      int64_t perm_numel, int64_t b_type_id, int64_t size_m, int64_t size_n,
+                      int64_t size_k, int is_zp_float) {
+  check(g_idx_numel == 0, "marlin_gemm does not support act_order g_idx.");
+  check(perm_numel == 0, "marlin_gemm does not support act_order perm.");
+  check_supported(is_half_type(a_dtype),
+                  "only float16 and bfloat16 activations are supported (8-bit activations are "
+                  "not implemented).");
+  check(a_scales_numel == 0, "a_scales can only be used for 8bit activation.");
+  const MetaCheck mc = check_weight_meta(b_type_id, a_dtype, b_scales_dtype, b_scales_numel,
+                                         num_groups, 1, global_scale, global_scale_numel, 1,
+                                         b_zeros, b_zeros_dtype, b_zeros_numel, is_zp_float,
+                                         size_n, size_k);
+  const int bits = fmt_bits(mc.fmt);
+  const int64_t pack = 32 / bits;
+  check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
+  check(b_q_weight_numel == size_k * size_n / pack, "Shape mismatch: b_q_weight numel = ",
+        b_q_weight_numel, ", size_k * size_n / pack_factor = ", size_k * size_n / pack);
+  check(size_k % 32 == 0, "marlin_gemm requires size_k % 32 == 0.");
+  check(size_n % 64 == 0, "marlin_gemm requires size_n % 64 == 0. size_n = ", size_n,
+        ", min_thread_n = ", 64);
+  check(a_row_stride % 8 == 0, "A.stride(0) must divisible by 8");
+  check(((uintptr_t)a) % 16 == 0, "A must aligned to 16 bytes");
+  check(b_bias_numel == 0 || b_bias_numel == size_n, "b_bias.size(0) != size_n");
+  check(size_m >= 0 && size_m <= INT32_MAX, "size_m out of range");
+  DenseCall d{};
+  d.empty = size_m == 0 || size_n == 0;
+  if (d.empty) return d;
+  check(size_k > 0, "size_k must be positive");
+  check(a && c && b_q_weight && b_scales, "null tensor pointer");
+
+  check_hip(hipGetDevice(&d.dev), "hipGetDevice");
+  d.plan = dense_plan(d.dev, mc.fmt, a_dtype == MARLIN_DTYPE_BFLOAT16, mc.gsm, size_m, size_n,
+                      size_k);
+  const Plan& plan = d.plan.plan;
+  GemmParams& p = d.params;
+  p.a = a;
+  p.a_stride = a_row_stride;
+  p.c = c;
+  p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
+  p.b_expert_stride = 0;
+  p.scales = b_scales;
+  p.zeros = b_zeros_numel ? b_zeros : nullptr;
+  p.meta_expert_stride = 0;
+  p.bias = b_bias_numel ? b_bias : nullptr;
+  p.global_scale = global_scale;
+  p.alpha_exp = 7 - (a_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
+  p.M = (int)size_m;
+  p.N = (int)size_n;
+  p.K = (int)size_k;
+  p.group_shift = mc.group_shift;
+  p.splits = plan.splits;
+  p.steps_per_split = plan.steps_per_split;
+  p.main_blocks = plan.main_blocks;
+  p.num_n_blocks = plan.n_blocks;
+  p.num_m_blocks = plan.m_blocks;
+  p.xcd_group_m = plan.xcd_group_m;
+  if (plan.splits > 1) {
+    d.ws_elems = (size_t)size_m * size_n;
+    d.ws_counters = (size_t)plan.m_blocks * plan.n_blocks;
+  }
+  return d;
+}
+
 }  // namespace
 
 extern "C" {
@@ -589,80 +824,21 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
   (void)use_atomic_add;
   (void)use_fp32_reduce;
   return guarded([&] {
-    check(g_idx_numel == 0, "marlin_gemm does not support act_order g_idx.");
-    check(perm_numel == 0, "marlin_gemm does not support act_order perm.");
-    check_supported(is_half_type(a_dtype),
-                    "only float16 and bfloat16 activations are supported (8-bit activations are "
-                    "not implemented).");
-    check(a_scales_numel == 0, "a_scales can only be used for 8bit activation.");
-    const MetaCheck mc = check_weight_meta(b_type_id, a_dtype, b_scales_dtype, b_scales_numel,
-                                           num_groups, 1, global_scale, global_scale_numel, 1,
-                                           b_zeros, b_zeros_dtype, b_zeros_numel, is_zp_float,
-                                           size_n, size_k);
-    const int bits = fmt_bits(mc.fmt);
-    const int64_t pack = 32 / bits;
-    check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
-    check(b_q_weight_numel == size_k * size_n / pack, "Shape mismatch: b_q_weight numel = ",
-          b_q_weight_numel, ", size_k * size_n / pack_factor = ", size_k * size_n / pack);
-    check(size_k % 32 == 0, "marlin_gemm requires size_k % 32 == 0.");
-    check(size_n % 64 == 0, "marlin_gemm requires size_n % 64 == 0. size_n = ", size_n,
-          ", min_thread_n = ", 64);
-    check(a_row_stride % 8 == 0, "A.stride(0) must divisible by 8");
-    check(((uintptr_t)a) % 16 == 0, "A must aligned to 16 bytes");
-    check(b_bias_numel == 0 || b_bias_numel == size_n, "b_bias.size(0) != size_n");
-    check(size_m >= 0 && size_m <= INT32_MAX, "size_m out of range");
-    if (size_m == 0 || size_n == 0) return;
-    check(size_k > 0, "size_k must be positive");
-    check(a && c && b_q_weight && b_scales, "null tensor pointer");
-
+    const DenseCall d = check_dense(a, a_dtype, a_row_stride, c, b_q_weight, b_q_weight_numel,
+                                    b_bias, b_bias_numel, b_scales, b_scales_dtype,
+                                    b_scales_numel, num_groups, a_scales_numel, global_scale,
+                                    global_scale_numel, b_zeros, b_zeros_dtype, b_zeros_numel,
+                                    g_idx_numel, perm_numel, b_type_id, size_m, size_n, size_k,
+                                    is_zp_float);
+    if (d.empty) return;
     hipStream_t s = (hipStream_t)stream;
-    int dev = 0;
-    check_hip(hipGetDevice(&dev), "hipGetDevice");
-    GemmLaunch l{};
-    l.fmt = mc.fmt;
-    l.bf16 = a_dtype == MARLIN_DTYPE_BFLOAT16;
-    l.gsm = mc.gsm;
-    const Plan plan = select_dense(size_m, size_n, size_k, device_cu_count(dev), l);
-
-    GemmParams p{};
-    p.a = a;
-    p.a_stride = a_row_stride;
-    p.c = c;
-    p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
-    p.b_expert_stride = 0;
-    p.scales = b_scales;
-    p.zeros = b_zeros_numel ? b_zeros : nullptr;
-    p.meta_expert_stride = 0;
-    p.bias = b_bias_numel ? b_bias : nullptr;
-    p.global_scale = global_scale;
-    p.alpha_exp = 7 - (a_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
-    p.M = (int)size_m;
-    p.N = (int)size_n;
-    p.K = (int)size_k;
-    p.group_shift = mc.group_shift;
-    p.splits = plan.splits;
-    p.steps_per_split = plan.steps_per_split;
-    p.main_blocks = plan.main_blocks;
-    p.num_n_blocks = plan.n_blocks;
-    p.num_m_blocks = plan.m_blocks;
-    p.xcd_group_m = plan.xcd_group_m;
-    if (plan.splits > 1) {
-      Workspace& w = get_workspace(dev, s, (size_t)size_m * size_n,
-                                   (size_t)plan.m_blocks * plan.n_blocks);
+    GemmParams p = d.params;
+    if (d.plan.plan.splits > 1) {
+      Workspace& w = get_workspace(d.dev, s, d.ws_elems, d.ws_counters);
       p.ws = w.ws;
       p.counters = w.counters;
     }
-    l.bm = plan.bm;
-    l.nt = plan.nt;
-    l.ch = plan.ch;
-    l.depth = plan.depth;
-    l.wpb = plan.wpb;
-    l.ksplit = plan.ksplit != 0;
-    l.occ = plan.occ;
-    l.stream = plan.stream != 0;
-    l.moe = false;
-    l.grid = (unsigned)plan.grid;
-    check_hip(dispatch_gemm(l, p, s), "marlin_gemm launch");
+    check_hip(dispatch_gemm(d.plan.launch, p, s), "marlin_gemm launch");
   });
 }
 
@@ -682,8 +858,14 @@ marlin_status_t marlin_moe_align_block_size(const void* topk_ids, marlin_dtype_t
     check(padded_num_experts <= 1024, "padded_num_experts must be at most 1024");
     check(block_size >= 1, "block_size must be positive");
     check(numel >= 0 && numel < INT32_MAX, "topk_ids numel out of range");
-    check(sorted_numel >= numel + num_experts * (block_size - 1) || sorted_numel >= numel,
-          "sorted_token_ids too small");
+    // the padded total reaches numel + E * (block_size - 1) in the worst case; a shorter
+    // buffer would drop routes (the reference sizes it so: moe_align_block_size.py:15)
+    const int64_t max_padded = numel + num_experts * (block_size - 1);
+    check(sorted_numel >= max_padded, "sorted_token_ids must hold numel + num_experts * "
+          "(block_size - 1) = ", max_padded, " entries, got ", sorted_numel);
+    check(expert_ids_numel >= (max_padded + block_size - 1) / block_size,
+          "experts_ids must hold ceil(max_num_tokens_padded / block_size) = ",
+          (max_padded + block_size - 1) / block_size, " entries, got ", expert_ids_numel);
     check(expert_map_numel == 0 || expert_map_numel >= num_experts,
           "expert_map must cover num_experts entries");
     check(sorted_token_ids && expert_ids && num_tokens_post_pad, "null output pointer");
@@ -764,12 +946,13 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     check_hip(hipGetDevice(&dev), "hipGetDevice");
     const int cus = device_cu_count(dev);
 
+    const Overrides& ov = overrides();
     const int bm = moe_block_size <= 16 ? 16 : (int)moe_block_size;  // 8 -> 16 rows
-    const int nt = 4;
-    check_supported(size_n % 256 == 0,
-                    "moe_wna16_marlin_gemm on this build requires size_n % 256 == 0");
+    // column blocks of the multistage kernel: 4 waves x nt n16 tiles; the widest that divides
+    // size_n (the reference requires size_n % 64, ops.cu:390-392)
+    const int nt = size_n % 256 == 0 ? 4 : (size_n % 128 == 0 ? 2 : 1);
     const int m_blocks = (int)((sorted_numel + moe_block_size - 1) / moe_block_size);
-    const int n_blocks = (int)(size_n / 256);
+    const int n_blocks = (int)(size_n / (64 * nt));
     const int steps = (int)(size_k / 128);
     // Only a fraction of the moe blocks are live; estimate them from the route count.
     const int64_t live = std::min<int64_t>(m_blocks, (size_m * top_k + moe_block_size - 1) /
@@ -779,7 +962,7 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     if (base < (int64_t)cus * 2 && steps >= 4) {
       splits = (int)std::min<int64_t>(((int64_t)cus * 2 + base - 1) / base, steps / 2);
     }
-    splits = env_int("MARLIN_MI355X_MOE_SPLIT_K", splits);
+    if (ov.moe_split_k >= 0) splits = ov.moe_split_k;
     splits = std::max(1, std::min(splits, std::max(steps, 1)));
     const int sps = steps == 0 ? 0 : (steps + splits - 1) / splits;
     splits = steps == 0 ? 1 : (steps + sps - 1) / sps;
@@ -808,7 +991,7 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     if (splits == 1) {
       // moe blocks of one expert (and their activation rows) in one L2: groups of
       // consecutive moe blocks x all column blocks dealt to the XCDs in turn
-      p.xcd_group_m = env_int("MARLIN_MI355X_MOE_GROUP_M", 4);
+      p.xcd_group_m = ov.moe_group_m;
       p.xcd_interleave = p.xcd_group_m > 0 ? 1 : 0;
     }
     p.sorted_ids = sorted_token_ids;
@@ -835,29 +1018,34 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     l.nt = nt;
     l.ch = 1;
     l.moe = true;
-    l.stream = !(mc.gsm == GSM_SMALL && bm >= 48) && env_int("MARLIN_MI355X_STREAM", 1) != 0;
+    // (small-group metadata of 48/64-row blocks over 256 columns does not fit the multistage
+    // kernel's registers: those blocks take the tiled kernel)
+    l.stream = !(mc.gsm == GSM_SMALL && bm >= 48 && nt == 4) && ov.stream != 0;
     l.grid = (unsigned)((int64_t)m_blocks * n_blocks * splits);
     // Few routes per expert (decode-sized batches): the K-split decode kernel, one moe block
     // and 64 columns per workgroup, multiplying only the block's 16-row parts that hold
     // routes.  Its integer-operand path needs integer or fp8 weights with >= 128-deep groups.
     const bool int_operand = mc.fmt != FMT_MXFP4 && mc.fmt != FMT_NVFP4 && mc.gsm != GSM_SMALL;
-    if (int_operand && size_m * top_k <= 16 * num_experts &&
-        env_int("MARLIN_MI355X_MOE_DECODE", 1) != 0) {
+    if (int_operand && size_m * top_k <= 16 * num_experts && ov.moe_decode != 0) {
       const int groups = (int)(size_n / 64);
       p.splits = 1;
       p.steps_per_split = steps;
       p.num_n_blocks = groups;
       p.num_m_blocks = m_blocks;
       l.stream = false;
-      l.depth = env_int("MARLIN_MI355X_MOE_DEPTH", 3);
+      l.depth = ov.moe_depth;
       l.nt = 4;
       // one wave per workgroup, all of K: thousands of short workgroups that the dispatcher
       // load-balances across CUs as they finish
-      l.wpb = env_int("MARLIN_MI355X_MOE_WPB", 1);
+      l.wpb = ov.moe_wpb;
       l.ksplit = true;
       l.occ = 1;
       l.grid = (unsigned)((int64_t)m_blocks * groups);
     }
+    if (ov.any && !instantiated(l))
+      check_supported(false, "no moe kernel instance for the selected configuration; a "
+                             "MARLIN_MI355X_* tuning override selects a configuration this "
+                             "build does not instantiate");
     check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");
   });
 }
@@ -900,13 +1088,15 @@ marlin_status_t marlin_moe_sum(const void* input, marlin_dtype_t dtype, int64_t 
                                int64_t top_k, int64_t hidden, void* out,
                                marlin_stream_t stream) {
   return guarded([&] {
-    check(is_half_type(dtype), "moe_sum supports float16 and bfloat16");
-    check(num_tokens >= 0 && top_k >= 1 && hidden >= 0, "invalid moe_sum shape");
-    check(num_tokens <= 65535, "moe_sum supports at most 65535 tokens per call");
+    check(is_half_type(dtype) || dtype == MARLIN_DTYPE_FLOAT32,
+          "moe_sum supports float16, bfloat16 and float32");
+    check(num_tokens >= 0 && top_k >= 1 && top_k <= INT32_MAX && hidden >= 0,
+          "invalid moe_sum shape");
     if (num_tokens == 0 || hidden == 0) return;
     check(input && out, "null tensor pointer");
-    check_hip(launch_moe_sum(input, dtype == MARLIN_DTYPE_BFLOAT16, num_tokens, (int)top_k, hidden,
-                             out, (hipStream_t)stream),
+    const int kind = dtype == MARLIN_DTYPE_FLOAT32 ? 2 : (dtype == MARLIN_DTYPE_BFLOAT16 ? 1 : 0);
+    check_hip(launch_moe_sum(input, kind, num_tokens, (int)top_k, hidden, out,
+                             (hipStream_t)stream),
               "moe_sum launch");
   });
 }

@@ -1,6 +1,6 @@
-// gemm_instances.h -- instantiation table of marlin_gemm_kernel for one weight format.
-// Included by gemm_<fmt>.hip with MMI_FMT and MMI_FN defined, so the formats compile in
-// parallel translation units.
+// gemm_instances.h -- instantiation table of the GEMM kernels for one weight format and one
+// activation type.  Included by gemm_<fmt>_<f16|bf16>.hip with MMI_FMT, MMI_AT and MMI_FN
+// defined, so the formats and activation types compile in parallel translation units.
 #include "host_common.h"
 
 namespace mmi {
@@ -53,10 +53,10 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     return hipErrorInvalidValue;
   }
   if (l.stream) {
-// (per-32/64 group metadata for 48/64-row blocks does not fit the register budget: those
-// stay on marlin_gemm_kernel)
+// (per-32/64 group metadata for 48/64-row blocks over 256 columns does not fit the register
+// budget: those stay on marlin_gemm_kernel)
 #define MMI_STREAM(BM_, NT_, MOE_)                                                          \
-  if constexpr (!(GSM == GSM_SMALL && BM_ >= 48)) {                                         \
+  if constexpr (!(GSM == GSM_SMALL && BM_ >= 48 && NT_ >= 4)) {                             \
     if (l.bm == BM_ && l.nt == NT_ && l.moe == MOE_)                                        \
       return launch_or_query(l, marlin_stream_kernel<FMT, AT, BM_, NT_, GSM, MOE_>, 256, p, s); \
   }
@@ -72,6 +72,15 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     MMI_STREAM(32, 4, true)
     MMI_STREAM(48, 4, true)
     MMI_STREAM(64, 4, true)
+    // MoE with size_n % 256 != 0: 128- and 64-column blocks
+    MMI_STREAM(16, 2, true)
+    MMI_STREAM(32, 2, true)
+    MMI_STREAM(48, 2, true)
+    MMI_STREAM(64, 2, true)
+    MMI_STREAM(16, 1, true)
+    MMI_STREAM(32, 1, true)
+    MMI_STREAM(48, 1, true)
+    MMI_STREAM(64, 1, true)
 #undef MMI_STREAM
     return hipErrorInvalidValue;
   }
@@ -110,8 +119,8 @@ static hipError_t launch_at(const GemmLaunch& l, const GemmParams& p, hipStream_
 }
 
 hipError_t MMI_FN(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
-  if (l.fmt != MMI_FMT) return hipErrorInvalidValue;
-  return l.bf16 ? launch_at<MMI_FMT, BF16>(l, p, s) : launch_at<MMI_FMT, F16>(l, p, s);
+  if (l.fmt != MMI_FMT || l.bf16 != (MMI_AT::kId == 1)) return hipErrorInvalidValue;
+  return launch_at<MMI_FMT, MMI_AT>(l, p, s);
 }
 
 }  // namespace mmi

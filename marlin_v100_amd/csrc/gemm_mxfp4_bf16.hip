@@ -1,0 +1,5 @@
+// gemm_mxfp4_bf16.hip -- GEMM kernel instances for mxfp4 weights and bf16 activations.
+#define MMI_FMT mmi::FMT_MXFP4
+#define MMI_AT mmi::BF16
+#define MMI_FN launch_gemm_mxfp4_bf16
+#include "gemm_instances.h"

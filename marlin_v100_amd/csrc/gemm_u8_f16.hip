@@ -1,0 +1,5 @@
+// gemm_u8_f16.hip -- GEMM kernel instances for u8 weights and f16 activations.
+#define MMI_FMT mmi::FMT_U8
+#define MMI_AT mmi::F16
+#define MMI_FN launch_gemm_u8_f16
+#include "gemm_instances.h"

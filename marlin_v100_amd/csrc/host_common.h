@@ -22,7 +22,8 @@ hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, i
                             int* post_pad, const int* expert_map, hipStream_t stream);
 hipError_t launch_silu_and_mul(const void* x, bool bf16, int64_t rows, int64_t d, void* out,
                                hipStream_t stream);
-hipError_t launch_moe_sum(const void* in, bool bf16, int64_t tokens, int topk, int64_t hidden,
+// kind: 0 fp16, 1 bf16, 2 fp32
+hipError_t launch_moe_sum(const void* in, int kind, int64_t tokens, int topk, int64_t hidden,
                           void* out, hipStream_t stream);
 // Router limits: experts per row held in one wavefront's registers, chosen experts per row.
 constexpr int kRouterMaxExperts = 64 * 64;
@@ -56,14 +57,18 @@ struct GemmLaunch {
   int* occupancy;  // when set: report workgroups per CU instead of launching
   int* scratch;    // with occupancy: also report the kernel's scratch bytes per lane
 };
-// Defined per format in gemm_<fmt>.hip; returns hipErrorInvalidValue for a configuration
-// that is not instantiated.
-hipError_t launch_gemm_u4b8(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm_u4(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm_u8b128(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm_u8(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm_fp8(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm_mxfp4(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm_nvfp4(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+// Defined per format and activation type in gemm_<fmt>_<f16|bf16>.hip; each returns
+// hipErrorInvalidValue for a configuration that is not instantiated.
+#define MMI_DECLARE_LAUNCH(F)                                                          \
+  hipError_t launch_gemm_##F##_f16(const GemmLaunch& l, const GemmParams& p, hipStream_t s); \
+  hipError_t launch_gemm_##F##_bf16(const GemmLaunch& l, const GemmParams& p, hipStream_t s);
+MMI_DECLARE_LAUNCH(u4b8)
+MMI_DECLARE_LAUNCH(u4)
+MMI_DECLARE_LAUNCH(u8b128)
+MMI_DECLARE_LAUNCH(u8)
+MMI_DECLARE_LAUNCH(fp8)
+MMI_DECLARE_LAUNCH(mxfp4)
+MMI_DECLARE_LAUNCH(nvfp4)
+#undef MMI_DECLARE_LAUNCH
 
 }  // namespace mmi

@@ -174,3 +174,57 @@ def test_grouped_topk_rejections():
     assert "bias size mismatch" in call(bias_numel=15)[1]
     st, err = call(e=2048, bias_numel=2048)
     assert st == 2 and "1024" in err
+
+
+def test_moe_align_buffer_size_rejections():
+    """A sorted_token_ids buffer shorter than numel + E * (bs - 1) would drop routes: it is
+    rejected before any launch (the reference sizes it so, moe_align_block_size.py:15)."""
+    lib = capi.load()
+    # numel 8, E 4, bs 16 -> needs 8 + 4 * 15 = 68 slots and ceil(68 / 16) = 5 expert ids
+    st = lib.marlin_moe_align_block_size(16, capi.I32, 8, 4, 16, 16, 67, 16, 5, 16, None, 0, None)
+    err = lib.marlin_get_last_error().decode()
+    assert st == 1 and "sorted_token_ids must hold" in err and "68" in err, err
+    st = lib.marlin_moe_align_block_size(16, capi.I32, 8, 4, 16, 16, 68, 16, 4, 16, None, 0, None)
+    err = lib.marlin_get_last_error().decode()
+    assert st == 1 and "experts_ids must hold" in err, err
+
+
+def test_moe_sum_dtypes():
+    lib = capi.load()
+    assert lib.marlin_moe_sum(16, capi.I32, 4, 2, 8, 16, None) == 1
+    assert "float16, bfloat16 and float32" in lib.marlin_get_last_error().decode()
+    # fp32 is accepted, and there is no token limit (nothing to launch at hidden 0)
+    assert lib.marlin_moe_sum(16, capi.F32, 1 << 20, 8, 0, 16, None) == 0
+
+
+def test_moe_size_n_multiple_of_64_is_accepted():
+    """size_n % 64 == 0 passes validation (reference ops.cu:390-392); without a GPU the call
+    then stops at the device query, not at a NOT_SUPPORTED size check."""
+    lib = capi.load()
+    e, n, k = 8, 320, 256
+    st = lib.marlin_moe_wna16_marlin_gemm(
+        16, capi.BF16, 16, 16, e * k * n // 8, e, None, 0, 16, capi.BF16, e * 2 * n, 2,
+        0, None, 0, 16, capi.BF16, e * 2 * n, 0, 0, None, 0, 16, 100, 16, 10, 16, 16, 64,
+        16, 4, 0, TYPE_ID["u4"], 16, n, k, 1, 0, 0, 1, -1, -1, -1, None)
+    err = lib.marlin_get_last_error().decode()
+    assert st != capi.STATUS_NOT_SUPPORTED and "256" not in err, (st, err)
+    st = lib.marlin_moe_wna16_marlin_gemm(
+        16, capi.BF16, 16, 16, e * k * 96 // 8, e, None, 0, 16, capi.BF16, e * 2 * 96, 2,
+        0, None, 0, 16, capi.BF16, e * 2 * 96, 0, 0, None, 0, 16, 100, 16, 10, 16, 16, 64,
+        16, 4, 0, TYPE_ID["u4"], 16, 96, k, 1, 0, 0, 1, -1, -1, -1, None)
+    assert st == 1 and "min_thread_n" in lib.marlin_get_last_error().decode()
+
+
+def test_product_scalar_type_round_trips_ids():
+    from marlin_v100_amd.scalar_type import NanRepr, ScalarType, scalar_types
+
+    for name in ("uint4", "uint4b8", "uint8", "uint8b128", "float4_e2m1f", "float8_e4m3fn",
+                 "float8_e8m0fnu"):
+        t = getattr(scalar_types, name)
+        assert ScalarType.from_id(t.id) == t and str(t) == name
+    odd = ScalarType(3, 2, True, 5, False, NanRepr.IEEE_754)
+    assert ScalarType.from_id(odd.id) == odd
+    with pytest.raises(ValueError):
+        ScalarType.from_id(-1)
+    with pytest.raises(ValueError):
+        ScalarType.from_id(1 << 60)

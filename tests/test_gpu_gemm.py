@@ -126,9 +126,11 @@ BASELINE_SHAPES = [
     ("cfg2", "u4", torch.bfloat16, 1024, 5120, 34816),
     ("cfg3", "u8b128", torch.float16, 4096, 8192, 8192),
     ("cfg4", "mxfp4", torch.bfloat16, 1, 3072, 12288),
+    ("cfg4", "mxfp4", torch.bfloat16, 64, 3072, 12288),
     ("cfg4", "mxfp4", torch.bfloat16, 512, 3072, 12288),
     ("cfg4", "nvfp4", torch.bfloat16, 1, 3072, 12288),
     ("cfg4", "nvfp4", torch.bfloat16, 64, 3072, 12288),
+    ("cfg4", "nvfp4", torch.bfloat16, 512, 3072, 12288),
 ]
 
 
@@ -141,3 +143,99 @@ def test_gemm_baseline_shapes(name, fmt, dtype, m, k, n):
     rows = torch.arange(m) if m <= 64 else torch.unique(torch.linspace(0, m - 1, 64).long())
     ref = O.gemm_ref(a[rows], case.deq)
     assert O.max_abs_rel_err(out[rows], ref) <= TOL
+
+
+# The tiled kernel (marlin_gemm_kernel) serves what the other two do not instantiate: M > 128
+# with N % 256 != 0 (16-row x 64-column tiles, split K when the grid is small) and groups
+# below 128 beyond M = 1024 (128 x 256 tiles).  K = 1056 leaves a 32-deep tail after the
+# 256-deep steps.
+TILED_CASES = [(fmt, dt, m, n, k) for fmt in ("u4b8", "u4", "u8b128", "fp8")
+               for dt in (torch.float16, torch.bfloat16)
+               for m, n, k in ((129, 192, 1024), (200, 320, 1024))]
+TILED_CASES += [("u8b128", torch.float16, 200, 320, 1056), ("u8b128", torch.bfloat16, 1500, 384, 1056)]
+
+
+@pytest.mark.parametrize("fmt,dtype,m,n,k", TILED_CASES)
+def test_gemm_tiled_kernel_narrow_n(fmt, dtype, m, n, k):
+    print(f"case tiled fmt={fmt} dtype={dtype} m={m} n={n} k={k}", flush=True)
+    case = make_case(fmt, k, n, dtype, seed=m + n + k)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(m + n)).to(dtype)
+    out = _run(case, a.cuda()).cpu()
+    assert O.max_abs_rel_err(out, _ref(case, a)) <= TOL
+
+
+@pytest.mark.parametrize("fmt,gs", [("u4", 32), ("u4b8", 64), ("mxfp4", None), ("nvfp4", None)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemm_tiled_kernel_small_groups_large_m(fmt, gs, dtype):
+    m, k, n = 1100, 1024, 512
+    print(f"case tiled-small-group fmt={fmt} gs={gs} dtype={dtype} m={m}", flush=True)
+    case = make_case(fmt, k, n, dtype, gs=gs, seed=77)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(78)).to(dtype)
+    out = _run(case, a.cuda()).cpu()
+    rows = torch.unique(torch.linspace(0, m - 1, 96).long())
+    assert O.max_abs_rel_err(out[rows], O.gemm_ref(a[rows], case.deq)) <= TOL
+
+
+_WIDE_CASES = {}
+
+
+def _wide_case(fmt, dtype):
+    key = (fmt, dtype)
+    if key not in _WIDE_CASES:
+        _WIDE_CASES[key] = make_case(fmt, 1024, 16384, dtype, seed=4242)
+    return _WIDE_CASES[key]
+
+
+@pytest.mark.parametrize("fmt", ["u4b8", "u4", "u8b128", "u8", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [2, 4, 8])
+def test_gemm_decode_wide_n(fmt, dtype, m):
+    """N = 16384: more 64-column groups than CUs, the decode kernel's three-waves-per-SIMD
+    instances (two steps in flight up to eight rows, or its depth-3 fallback)."""
+    print(f"case wide-n fmt={fmt} dtype={dtype} m={m}", flush=True)
+    case = _wide_case(fmt, dtype)
+    a = torch.randn((m, case.k), generator=torch.Generator().manual_seed(m)).to(dtype)
+    out = _run(case, a.cuda()).cpu()
+    assert O.max_abs_rel_err(out, _ref(case, a)) <= TOL
+
+
+def test_gemm_graph_capture_on_side_stream():
+    """A split-K shape captured into a HIP graph on a side stream after one eager call on
+    that stream: every replay (with eager work and syncs between) equals the eager output.
+    Capturing a shape whose workspace was never sized on the capturing stream is a clean
+    error, not an allocation inside the capture."""
+    k, n, m = 8192, 256, 4
+    case = make_case("u4b8", k, n, torch.float16, seed=11)
+    d = to_dev(case)
+    words = capi.gptq_marlin_repack(d.gptq_words, None, k, n, 4)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(3)).half().cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = capi.marlin_gemm(a, words, d.scales, case.type_id, m, n, k)
+        c = torch.empty_like(eager)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            capi.marlin_gemm(a, words, d.scales, case.type_id, m, n, k, c=c)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    ref = eager.cpu()
+    for i in range(4):
+        c.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        other = capi.marlin_gemm(a, words, d.scales, case.type_id, m, n, k)  # eager work between
+        torch.cuda.synchronize()
+        assert O.max_abs_rel_err(c.cpu(), ref) <= 1e-3, i
+        assert O.max_abs_rel_err(other.cpu(), ref) <= 1e-3, i
+    assert O.max_abs_rel_err(ref, _ref(case, a.cpu())) <= TOL
+
+    # a fresh stream has no workspace: capture must fail cleanly
+    fresh = torch.cuda.Stream()
+    fresh.wait_stream(torch.cuda.current_stream())
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(capi.MarlinError, match="capturing stream"):
+        with torch.cuda.graph(g2, stream=fresh):
+            capi.marlin_gemm(a, words, d.scales, case.type_id, m, n, k, c=c)
+    torch.cuda.synchronize()

@@ -211,3 +211,122 @@ def test_moe_sum(dtype, topk, tokens, hidden):
         o = torch.empty((1, hidden), dtype=dtype, device="cuda")
         capi.moe_sum(kat.cuda(), o)
         assert (o.cpu() == 1.0).all()
+
+
+def _moe_ref(x, deq, ids, topk, tw=None, mul=False):
+    """fp32 oracle per route: row r uses token r // topk and expert ids.flat[r]."""
+    flat = ids.reshape(-1)
+    ref = torch.empty((flat.numel(), deq.shape[-1]))
+    for r in range(flat.numel()):
+        ref[r] = x[r // topk].float() @ deq[flat[r]].float()
+        if mul:
+            ref[r] *= tw.reshape(-1)[r]
+    return ref
+
+
+@pytest.mark.parametrize("fmt", ["u4", "u4b8", "u8b128"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bs", [16, 32, 48, 64])
+def test_moe_gemm_multistage_integer(fmt, dtype, bs):
+    """More than 16 routes per expert on average (T * top_k > 16 * E): the multistage MoE
+    blocks with integer weights, every route against the oracle's dequantized experts."""
+    T, E, topk, H, N = 96, 4, 2, 256, 512
+    print(f"case moe-multistage fmt={fmt} dtype={dtype} bs={bs}", flush=True)
+    tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, H, N, dtype, 40)
+    gen = torch.Generator().manual_seed(bs + 7)
+    x = torch.randn((T, H), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    for mul in (False, True):
+        out = capi.moe_wna16_marlin_gemm(x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(),
+                                         tw.cuda(), bs, topk, mul, tid, T, N, H, b_zeros=zeros,
+                                         global_scale=glob, is_zp_float=zeros is not None).cpu()
+        assert O.max_abs_rel_err(out, _moe_ref(x, deq, ids, topk, tw, mul)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["u4", "u8b128", "mxfp4", "nvfp4"])
+@pytest.mark.parametrize("n", [320, 384])
+@pytest.mark.parametrize("T,bs", [(5, 16), (96, 16), (96, 48), (96, 64)])
+def test_moe_gemm_size_n_multiple_of_64(fmt, n, T, bs):
+    """size_n % 256 != 0 (the reference accepts size_n % 64, ops.cu:390-392): 64- and
+    128-column blocks of the multistage kernel, and the few-routes kernel."""
+    E, topk, H = 4, 2, 256
+    dtype = torch.bfloat16
+    print(f"case moe-narrow fmt={fmt} n={n} T={T} bs={bs}", flush=True)
+    tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, H, n, dtype, 50)
+    gen = torch.Generator().manual_seed(T + bs)
+    x = torch.randn((T, H), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    out = capi.moe_wna16_marlin_gemm(x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(),
+                                     tw.cuda(), bs, topk, False, tid, T, n, H, b_zeros=zeros,
+                                     global_scale=glob, is_zp_float=zeros is not None).cpu()
+    assert O.max_abs_rel_err(out, _moe_ref(x, deq, ids, topk)) <= TOL
+
+
+@pytest.mark.parametrize("topk", [1, 3, 4, 8])
+def test_moe_sum_fp32(topk):
+    gen = torch.Generator().manual_seed(topk)
+    x = torch.randn((37, topk, 200), generator=gen)
+    out = torch.empty((37, 200), device="cuda")
+    capi.moe_sum(x.cuda(), out)
+    ref = x[:, 0].clone()
+    for j in range(1, topk):
+        ref += x[:, j]  # fp32 additions in index order
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_moe_sum_many_tokens():
+    """More than 65535 tokens in one call (no grid-dimension limit), odd hidden size."""
+    tokens, topk, hidden = 70001, 2, 3
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn((tokens, topk, hidden), generator=gen).to(torch.bfloat16)
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device="cuda")
+    capi.moe_sum(x.cuda(), out)
+    assert torch.equal(out.cpu(), O.moe_sum(x))
+
+
+def test_fused_marlin_moe_reference_keywords():
+    """The reference's keyword set (fused_marlin_moe.py:217-255): activation, moe_sum,
+    workspace, intermediate caches, output, is_k_full, input_dtype, inplace; a custom
+    activation callback; act-order arguments raise NotImplementedError."""
+    from marlin_v100_amd import _custom_ops as cops
+    from marlin_v100_amd.fused_marlin_moe import (MoEActivation, apply_moe_activation,
+                                                  fused_marlin_moe)
+
+    T, E, topk, H, I = 17, 8, 2, 256, 128
+    dtype = torch.bfloat16
+    tid, w13, s13, z13, _, d13 = _make_experts("u4", E, H, 2 * I, dtype, 70)
+    _, w2, s2, z2, _, d2 = _make_experts("u4", E, I, H, dtype, 90)
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn((T, H), generator=gen).to(dtype).cuda()
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    tw, ids = tw.cuda(), ids.cuda()
+    ref = O.moe_layer_ref(x.cpu(), d13, d2, tw.cpu(), ids.cpu())
+    cache13 = torch.empty((T * topk * max(2 * I, H),), dtype=dtype, device="cuda")
+    cache2 = torch.empty((T * topk, I), dtype=dtype, device="cuda")
+    out = torch.empty((T, H), dtype=dtype, device="cuda")
+    got = fused_marlin_moe(
+        hidden_states=x, w1=w13, w2=w2, bias1=None, bias2=None, w1_scale=s13, w2_scale=s2,
+        topk_weights=tw, topk_ids=ids, quant_type_id=tid, apply_router_weight_on_input=False,
+        global_num_experts=-1, activation=MoEActivation.SILU, moe_sum=cops.moe_sum,
+        expert_map=None, global_scale1=None, global_scale2=None, g_idx1=None, g_idx2=None,
+        sort_indices1=None, sort_indices2=None, w1_zeros=z13, w2_zeros=z2, is_w1_zp_float=True,
+        is_w2_zp_float=True, workspace=None, intermediate_cache13=cache13,
+        intermediate_cache2=cache2, is_k_full=True, output=out, input_dtype=None, inplace=False)
+    assert O.max_abs_rel_err(out.cpu(), ref) <= 2 * TOL
+    calls = []
+
+    def act(a, o, i):
+        calls.append(a)
+        apply_moe_activation(a, o, i)
+
+    got2 = fused_marlin_moe(x, w13, w2, None, None, s13, s2, tw, ids, tid, False, -1,
+                            MoEActivation.SILU, act, w1_zeros=z13, w2_zeros=z2,
+                            is_w1_zp_float=True, is_w2_zp_float=True)
+    assert calls == [MoEActivation.SILU]
+    assert O.max_abs_rel_err(got2.cpu(), ref) <= 2 * TOL
+    with pytest.raises(NotImplementedError):
+        fused_marlin_moe(x, w13, w2, None, None, s13, s2, tw, ids, tid,
+                         g_idx1=torch.zeros(H, dtype=torch.int32, device="cuda"),
+                         w1_zeros=z13, w2_zeros=z2, is_w1_zp_float=True, is_w2_zp_float=True)
