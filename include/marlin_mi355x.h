@@ -115,6 +115,32 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
                             marlin_stream_t stream);
 
 /*
+ * marlin_gemm for callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the reference.
+ * Same arguments, checks and results as marlin_gemm (minus the ignored workspace and
+ * reduction flags), but it calls no hipMalloc / hipFree / allocating library routine: the
+ * split-K partial sums and arrival counters live in a static device array of fixed size,
+ * one per GPU, held until the process ends.  A call whose plan splits K and needs more than
+ * MARLIN_NO_ALLOC_MAX_PARTIALS partial sums (size_m * size_n) or MARLIN_NO_ALLOC_MAX_COUNTERS
+ * counters returns MARLIN_STATUS_INVALID_ARGUMENT.  The first call on a device clears the
+ * array with one fill kernel on `stream`.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or host threads) race.
+ */
+#define MARLIN_NO_ALLOC_MAX_PARTIALS 2097152
+#define MARLIN_NO_ALLOC_MAX_COUNTERS 65536
+marlin_status_t marlin_gemm_no_alloc(const void* a, marlin_dtype_t a_dtype, int64_t a_row_stride,
+                                     void* c, const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                     const void* b_bias, int64_t b_bias_numel,
+                                     const void* b_scales, marlin_dtype_t b_scales_dtype,
+                                     int64_t b_scales_numel, int64_t num_groups,
+                                     int64_t a_scales_numel, const float* global_scale,
+                                     int64_t global_scale_numel, const void* b_zeros,
+                                     marlin_dtype_t b_zeros_dtype, int64_t b_zeros_numel,
+                                     int64_t g_idx_numel, int64_t perm_numel, int64_t b_type_id,
+                                     int64_t size_m, int64_t size_n, int64_t size_k,
+                                     int is_zp_float, marlin_stream_t stream);
+
+/*
  * MoE token alignment: sorts the flat route indices of topk_ids by expert and pads each
  * expert's run to a multiple of block_size.
  * Replaces torch.ops._moe_C.moe_align_block_size

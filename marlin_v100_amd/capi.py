@@ -40,6 +40,9 @@ SIGNATURES = {
     "marlin_gemm": (_I, [_P, _I, _I64, _P, _P, _I64, _P, _I64, _P, _I, _I64, _I64, _I64, _P, _I64,
                          _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
                          _I, _P]),
+    "marlin_gemm_no_alloc": (_I, [_P, _I, _I64, _P, _P, _I64, _P, _I64, _P, _I, _I64, _I64,
+                                  _I64, _P, _I64, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64,
+                                  _I64, _I, _P]),
     "marlin_moe_align_block_size": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P,
                                          _I64, _P]),
     "marlin_moe_wna16_marlin_gemm": (_I, [_P, _I, _P, _P, _I64, _I64, _P, _I64, _P, _I, _I64,
@@ -136,6 +139,21 @@ def marlin_gemm(a, b_q_weight, b_scales, b_type_id, size_m, size_n, size_k, *, c
         b_scales.shape[0], _numel(a_scales), _ptr(global_scale), _numel(global_scale),
         _ptr(zeros), _dt(zeros), _numel(zeros), _numel(g_idx), _numel(perm), None, 0, b_type_id,
         size_m, size_n, size_k, 1, 0, 0, int(is_zp_float), _stream()))
+    return c
+
+
+def marlin_gemm_no_alloc(a, b_q_weight, b_scales, b_type_id, size_m, size_n, size_k, *, c=None,
+                         b_bias=None, global_scale=None, b_zeros=None, is_zp_float=False):
+    """marlin_gemm through the entry point that allocates no device memory (the split-K
+    scratch is the library's static per-GPU array)."""
+    if c is None:
+        c = torch.empty((size_m, size_n), dtype=a.dtype, device=a.device)
+    zeros = b_zeros if (b_zeros is not None and b_zeros.numel()) else None
+    _check(load().marlin_gemm_no_alloc(
+        _ptr(a), _dt(a), a.stride(0), _ptr(c), _ptr(b_q_weight), b_q_weight.numel(),
+        _ptr(b_bias), _numel(b_bias), _ptr(b_scales), _dt(b_scales), b_scales.numel(),
+        b_scales.shape[0], 0, _ptr(global_scale), _numel(global_scale), _ptr(zeros), _dt(zeros),
+        _numel(zeros), 0, 0, b_type_id, size_m, size_n, size_k, int(is_zp_float), _stream()))
     return c
 
 

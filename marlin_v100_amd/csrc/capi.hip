@@ -167,6 +167,43 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
   return w;
 }
 
+// ---- static split-K scratch of marlin_gemm_no_alloc -------------------------------------
+// One array per GPU, held until the process ends: kScratchPartials fp32 partial sums, then
+// kScratchCounters arrival counters.  A static __device__ array starts zeroed when the code
+// object loads, and the kernels' split-K protocol leaves every entry it used zeroed again
+// (the last arriver reads the sums back with atomic exchanges against 0 and resets its
+// counter), so each call finds it zeroed.  Calls that overlap on one GPU share the array
+// and race.
+constexpr size_t kScratchPartials = size_t(1) << 21;  // 8 MiB of fp32 partial sums
+constexpr size_t kScratchCounters = size_t(1) << 16;  // 256 KiB of arrival counters
+static_assert(kScratchPartials == MARLIN_NO_ALLOC_MAX_PARTIALS, "header limit");
+static_assert(kScratchCounters == MARLIN_NO_ALLOC_MAX_COUNTERS, "header limit");
+static __device__ __align__(256) uint32_t scratch[kScratchPartials + kScratchCounters];
+
+__global__ void clear_words(uint32_t* p, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// Device address of this GPU's scratch (the host-side name of the array is not one).  The
+// first call on a device, with that device current, looks the address up and clears the
+// array once with a fill kernel on the caller's stream (no allocation, no memset node).
+uint32_t* scratch_on_device(int dev, hipStream_t stream) {
+  static std::mutex mu;
+  static std::map<int, uint32_t*> ptrs;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = ptrs.find(dev);
+  if (it != ptrs.end()) return it->second;
+  void* ptr = nullptr;
+  check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  hipLaunchKernelGGL(clear_words, dim3(1024), dim3(256), 0, stream,
+                     reinterpret_cast<uint32_t*>(ptr), kScratchPartials + kScratchCounters);
+  check_hip(hipGetLastError(), "scratch clear launch");
+  ptrs[dev] = reinterpret_cast<uint32_t*>(ptr);
+  return ptrs[dev];
+}
+
 // ---- tile selection -------------------------------------------------------------------
 struct Plan {
   int bm, nt, ch, depth, wpb, ksplit, occ, stream, splits, steps_per_split, main_blocks, n_blocks,
@@ -839,6 +876,41 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
       p.counters = w.counters;
     }
     check_hip(dispatch_gemm(d.plan.launch, p, s), "marlin_gemm launch");
+  });
+}
+
+marlin_status_t marlin_gemm_no_alloc(const void* a, marlin_dtype_t a_dtype, int64_t a_row_stride,
+                                     void* c, const int32_t* b_q_weight, int64_t b_q_weight_numel,
+                                     const void* b_bias, int64_t b_bias_numel,
+                                     const void* b_scales, marlin_dtype_t b_scales_dtype,
+                                     int64_t b_scales_numel, int64_t num_groups,
+                                     int64_t a_scales_numel, const float* global_scale,
+                                     int64_t global_scale_numel, const void* b_zeros,
+                                     marlin_dtype_t b_zeros_dtype, int64_t b_zeros_numel,
+                                     int64_t g_idx_numel, int64_t perm_numel, int64_t b_type_id,
+                                     int64_t size_m, int64_t size_n, int64_t size_k,
+                                     int is_zp_float, marlin_stream_t stream) {
+  return guarded([&] {
+    const DenseCall d = check_dense(a, a_dtype, a_row_stride, c, b_q_weight, b_q_weight_numel,
+                                    b_bias, b_bias_numel, b_scales, b_scales_dtype,
+                                    b_scales_numel, num_groups, a_scales_numel, global_scale,
+                                    global_scale_numel, b_zeros, b_zeros_dtype, b_zeros_numel,
+                                    g_idx_numel, perm_numel, b_type_id, size_m, size_n, size_k,
+                                    is_zp_float);
+    if (d.empty) return;
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* base = scratch_on_device(d.dev, s);
+    GemmParams p = d.params;
+    if (d.plan.plan.splits > 1) {
+      check(d.ws_elems <= kScratchPartials && d.ws_counters <= kScratchCounters,
+            "marlin_gemm_no_alloc: this shape splits K and needs ", d.ws_elems,
+            " fp32 partial sums (size_m * size_n) and ", d.ws_counters,
+            " counters; the static scratch holds ", kScratchPartials, " and ",
+            kScratchCounters);
+      p.ws = reinterpret_cast<float*>(base);
+      p.counters = reinterpret_cast<int*>(base + kScratchPartials);
+    }
+    check_hip(dispatch_gemm(d.plan.launch, p, s), "marlin_gemm_no_alloc launch");
   });
 }
 
