@@ -173,12 +173,16 @@ def time_calls(fn_list, steps, warmup):
 def time_graph(fn_list, steps, warmup, per_graph=None):
     """Average per-call device time with the host out of the loop: the rotating calls are
     captured into one HIP graph on a side stream (after an eager warm-up of every call on
-    that stream, so no workspace is sized inside the capture) and the graph is replayed;
-    HIP events are recorded on that same stream.  Returns (seconds per call, calls)."""
+    that stream, so no workspace is sized inside the capture) and the graph is replayed.
+    A bounded spin kernel (torch.cuda._sleep) queued ahead of the start event keeps the
+    stream busy while the host submits the replays, so the events time back-to-back kernels
+    and not the graph's submission.  HIP events are recorded on that same stream.
+    Returns (seconds per call, calls timed)."""
     import torch
 
     n = len(fn_list)
     per_graph = per_graph or n * max(1, -(-50 // n))  # whole rotations, >= 50 calls
+    replays = max(1, -(-steps // per_graph))
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -189,11 +193,11 @@ def time_graph(fn_list, steps, warmup, per_graph=None):
         with torch.cuda.graph(graph, stream=side):
             for i in range(per_graph):
                 fn_list[i % n]()
-        replays = max(2, -(-steps // per_graph))
-        graph.replay()
+        graph.replay()  # first replay uploads the graph (untimed)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(SPIN_CYCLES)
         start.record(side)
         for _ in range(replays):
             graph.replay()
@@ -203,11 +207,15 @@ def time_graph(fn_list, steps, warmup, per_graph=None):
     return start.elapsed_time(end) / 1e3 / (replays * per_graph), replays * per_graph
 
 
+# spin ahead of a timed graph (tens of ms at GPU clock rates; longer than submitting the
+# replays of one measurement)
+SPIN_CYCLES = 50_000_000
+
 # calls shorter than this are timed from a captured graph (host dispatch would set the pace)
 GRAPH_BELOW_US = 60.0
 
 
-def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
+def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed, exact_steps=False):
     import torch
 
     from marlin_v100_amd import ops
@@ -237,7 +245,8 @@ def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
     t = time_calls(fns, steps, warmup)
     timing = "eager"
     if t * 1e6 < GRAPH_BELOW_US:
-        t, _ = time_graph(fns, steps, warmup)
+        # one graph of exactly `steps` calls (the headline's K steps), replayed once
+        t, _ = time_graph(fns, steps, warmup, per_graph=steps if exact_steps else None)
         timing = "graph"
     alg_bytes = wbytes + a.numel() * 2 + c.numel() * 2
     flops = 2.0 * m * n * k
@@ -408,7 +417,8 @@ def main() -> int:
 
     only = set(filter(None, args.only.split(",")))
     bf, hf = torch.bfloat16, torch.float16
-    head = dense_case("cfg2_m16", "u4", 16, 5120, 34816, bf, args.steps, args.warmup, 1002)
+    head = dense_case("cfg2_m16", "u4", 16, 5120, 34816, bf, args.steps, args.warmup, 1002,
+                      exact_steps=True)
 
     plan = [
         ("cfg1_m16", "u4b8", 16, 4096, 4096, hf, 1001),
