@@ -4,9 +4,9 @@ Headline (`value`): weight GB/s of marlin_gemm on BASELINE configs[1] -- AWQ-sty
 float zero point, group 128, bf16 activations, K=5120, N=34816 -- at M=16 (decode).  One
 "step" is one marlin_gemm call on that workload with all inputs resident in HBM.  Weight
 copies rotate through >= 512 MiB so the 256 MB Infinity Cache cannot hold them.  Calls
-shorter than 60 us are timed from a captured HIP graph of the rotating calls (host dispatch
-would otherwise set the pace); longer ones eagerly.  Both time with HIP events on the
-stream the kernels run on.
+shorter than 60 us are queued behind a spin kernel so they run back to back (host dispatch
+would otherwise set the pace); longer ones are timed eagerly.  Both time exactly the K
+calls with HIP events on the stream the kernels run on.
 
 The same JSON line carries every other BASELINE configuration (`configs`): cfg1 u4b8 fp16,
 cfg2 at M in {1,16,128,1024}, cfg3 u8b128 M=4096 (MFMA bound), cfg4 MXFP4/NVFP4 at
@@ -170,52 +170,38 @@ def time_calls(fn_list, steps, warmup):
     return start.elapsed_time(end) / 1e3 / steps
 
 
-def time_graph(fn_list, steps, warmup, per_graph=None):
-    """Average per-call device time with the host out of the loop: the rotating calls are
-    captured into one HIP graph on a side stream (after an eager warm-up of every call on
-    that stream, so no workspace is sized inside the capture) and the graph is replayed.
-    A bounded spin kernel (torch.cuda._sleep) queued ahead of the start event keeps the
-    stream busy while the host submits the replays, so the events time back-to-back kernels
-    and not the graph's submission.  HIP events are recorded on that same stream.
-    Returns (seconds per call, calls timed)."""
+def time_queued(fn_list, steps, warmup):
+    """Average per-call device time with the host out of the critical path: after an eager
+    warm-up, a bounded spin kernel (torch.cuda._sleep) is queued ahead of the start event, so
+    the GPU is busy while the host enqueues the K timed calls; they then run back to back and
+    the HIP events (on the stream the kernels run on) time the kernels, not the host's
+    dispatch rate.  No graph: on this stack a captured graph adds a per-node gap."""
     import torch
 
     n = len(fn_list)
-    per_graph = per_graph or n * max(1, -(-50 // n))  # whole rotations, >= 50 calls
-    replays = max(1, -(-steps // per_graph))
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(max(warmup, n)):
-            fn_list[i % n]()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=side):
-            for i in range(per_graph):
-                fn_list[i % n]()
-        graph.replay()  # first replay uploads the graph (untimed)
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(SPIN_CYCLES)
-        start.record(side)
-        for _ in range(replays):
-            graph.replay()
-        end.record(side)
-        torch.cuda.synchronize()
-    torch.cuda.current_stream().wait_stream(side)
-    return start.elapsed_time(end) / 1e3 / (replays * per_graph), replays * per_graph
+    for i in range(warmup):
+        fn_list[i % n]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SPIN_CYCLES)
+    start.record()
+    for i in range(steps):
+        fn_list[i % n]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
 
 
-# spin ahead of a timed graph (tens of ms at GPU clock rates; longer than submitting the
-# replays of one measurement)
+# spin ahead of the timed calls (tens of ms at GPU clock rates; longer than enqueueing them)
 SPIN_CYCLES = 50_000_000
 
-# calls shorter than this are timed from a captured graph (host dispatch would set the pace)
-GRAPH_BELOW_US = 60.0
+# calls shorter than this are timed with the host queued ahead (host dispatch would
+# otherwise set the pace)
+QUEUED_BELOW_US = 60.0
 
 
-def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed, exact_steps=False):
+def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed):
     import torch
 
     from marlin_v100_amd import ops
@@ -244,10 +230,9 @@ def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed, exact_steps=False)
     fns = [call(wt) for wt in weights]
     t = time_calls(fns, steps, warmup)
     timing = "eager"
-    if t * 1e6 < GRAPH_BELOW_US:
-        # one graph of exactly `steps` calls (the headline's K steps), replayed once
-        t, _ = time_graph(fns, steps, warmup, per_graph=steps if exact_steps else None)
-        timing = "graph"
+    if t * 1e6 < QUEUED_BELOW_US:
+        t = time_queued(fns, steps, warmup)
+        timing = "queued"
     alg_bytes = wbytes + a.numel() * 2 + c.numel() * 2
     flops = 2.0 * m * n * k
     gbs = alg_bytes / t / 1e9
@@ -329,9 +314,9 @@ def router_case(key, tokens, steps, warmup, seed, grouped=False):
             ops.topk_softmax(w, ids, tei, logits, True, None)
 
     # eager calls are bound by host dispatch (torch op -> C ABI -> launch); the device rate
-    # comes from a captured graph of 50 back-to-back calls (the kernel writes no memset node)
+    # comes from the same calls queued behind a spin kernel
     t_eager = time_calls([fn], steps, warmup)
-    t, _ = time_graph([fn], steps, warmup, per_graph=50)
+    t = time_queued([fn], steps, warmup)
     alg_bytes = tokens * E * 4 + tokens * topk * 12
     return {"key": key, "T": tokens, "E": E, "topk": topk, "us": round(t * 1e6, 2),
             "us_eager_dispatch": round(t_eager * 1e6, 2), "alg_bytes": alg_bytes,
@@ -417,8 +402,7 @@ def main() -> int:
 
     only = set(filter(None, args.only.split(",")))
     bf, hf = torch.bfloat16, torch.float16
-    head = dense_case("cfg2_m16", "u4", 16, 5120, 34816, bf, args.steps, args.warmup, 1002,
-                      exact_steps=True)
+    head = dense_case("cfg2_m16", "u4", 16, 5120, 34816, bf, args.steps, args.warmup, 1002)
 
     plan = [
         ("cfg1_m16", "u4b8", 16, 4096, 4096, hf, 1001),
