@@ -53,7 +53,7 @@ const char* marlin_get_last_error(void);
 
 /* ABI version of this header; bumped on incompatible changes. */
 int marlin_abi_version(void);
-#define MARLIN_MI355X_ABI_VERSION 1
+#define MARLIN_MI355X_ABI_VERSION 2
 
 /*
  * Weight repack: GPTQ layout [size_k / (32/num_bits), size_n] int32 (values packed LSB-first
@@ -91,9 +91,19 @@ marlin_status_t marlin_awq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_
  *               (NVFP4, S0E5M3-processed) or float8_e8m0fnu (MXFP4) for float4_e2m1f.
  *   a_scales_numel: must be 0 (8-bit activations are not supported, as in the reference).
  *   global_scale: NVFP4 only, fp32 numel 1.
- *   b_zeros   : uint4/uint8 only, float zero points [num_groups, size_n] in the dtype of a,
- *               is_zp_float must be 1.
- *   g_idx_numel, perm_numel: must be 0 (no act-order, as in the reference).
+ *   b_zeros   : uint4/uint8 only (and required there): float zero points [num_groups, size_n]
+ *               in the dtype of a with is_zp_float = 1, or integer zero points packed along N
+ *               as int32 [num_groups, size_n / (32/bits)] (column n in bits
+ *               [bits*(n % (32/bits)), ...)) with is_zp_float = 0; the latter dequantizes to
+ *               the single rounding of (q - z) * s.  The SM70 reference rejects packed integer
+ *               zero points (marlin.cu:336-339); upstream marlin takes them.
+ *   g_idx, perm: act-order, both [size_k] int32 or both absent: perm = argsort(original g_idx),
+ *               g_idx the sorted group index (marlin_sort_g_idx), the weights repacked with
+ *               perm.  Every group must hold group_size rows (GPTQ act-order), i.e.
+ *               g_idx[j] == j / group_size; columns that break it come out NaN.  A is gathered
+ *               by perm into a library staging buffer before the GEMM.  Integer weight types
+ *               and is_k_full = 1 only.  The reference rejects
+ *               act-order (marlin.cu:95-102); upstream marlin takes it.
  *   workspace : accepted for ABI fidelity and ignored, as in the reference (marlin.cu:103);
  *               split-K scratch is owned by the library per (device, stream).
  *   b_type_id : vllm ScalarType id (uint4, uint4b8, uint8, uint8b128, float8_e4m3fn,
@@ -108,11 +118,11 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
                             int64_t a_scales_numel,
                             const float* global_scale, int64_t global_scale_numel,
                             const void* b_zeros, marlin_dtype_t b_zeros_dtype,
-                            int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel,
-                            void* workspace, int64_t workspace_bytes, int64_t b_type_id,
-                            int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
-                            int use_atomic_add, int use_fp32_reduce, int is_zp_float,
-                            marlin_stream_t stream);
+                            int64_t b_zeros_numel, const int32_t* g_idx, int64_t g_idx_numel,
+                            const int32_t* perm, int64_t perm_numel, void* workspace,
+                            int64_t workspace_bytes, int64_t b_type_id, int64_t size_m,
+                            int64_t size_n, int64_t size_k, int is_k_full, int use_atomic_add,
+                            int use_fp32_reduce, int is_zp_float, marlin_stream_t stream);
 
 /*
  * marlin_gemm for callers that cannot allocate device memory: code under HIP graph capture,
@@ -124,7 +134,9 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
  * MARLIN_NO_ALLOC_MAX_PARTIALS partial sums (size_m * size_n) or MARLIN_NO_ALLOC_MAX_COUNTERS
  * counters returns MARLIN_STATUS_INVALID_ARGUMENT.  The first call on a device clears the
  * array with one fill kernel on `stream`.  Every call on a GPU shares that GPU's array:
- * calls that overlap on one GPU (different streams, or host threads) race.
+ * calls that overlap on one GPU (different streams, or host threads) race.  Act-order
+ * (g_idx_numel or perm_numel non-zero) returns MARLIN_STATUS_NOT_SUPPORTED: its activation
+ * staging buffer would need an allocation.
  */
 #define MARLIN_NO_ALLOC_MAX_PARTIALS 2097152
 #define MARLIN_NO_ALLOC_MAX_COUNTERS 65536

@@ -38,8 +38,8 @@ SIGNATURES = {
     "marlin_gptq_marlin_repack": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P]),
     "marlin_awq_marlin_repack": (_I, [_P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P]),
     "marlin_gemm": (_I, [_P, _I, _I64, _P, _P, _I64, _P, _I64, _P, _I, _I64, _I64, _I64, _P, _I64,
-                         _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
-                         _I, _P]),
+                         _P, _I, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I,
+                         _I, _I, _I, _P]),
     "marlin_gemm_no_alloc": (_I, [_P, _I, _I64, _P, _P, _I64, _P, _I64, _P, _I, _I64, _I64,
                                   _I64, _P, _I64, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64,
                                   _I64, _I, _P]),
@@ -129,16 +129,19 @@ def awq_marlin_repack(b_q_weight, size_k, size_n, num_bits, is_a_8bit=False, out
 
 def marlin_gemm(a, b_q_weight, b_scales, b_type_id, size_m, size_n, size_k, *, c=None,
                 b_bias=None, global_scale=None, b_zeros=None, is_zp_float=False, a_scales=None,
-                g_idx=None, perm=None):
+                g_idx=None, perm=None, is_k_full=True):
     if c is None:
         c = torch.empty((size_m, size_n), dtype=a.dtype, device=a.device)
     zeros = b_zeros if (b_zeros is not None and b_zeros.numel()) else None
+    g_idx = g_idx if (g_idx is not None and g_idx.numel()) else None
+    perm = perm if (perm is not None and perm.numel()) else None
     _check(load().marlin_gemm(
         _ptr(a), _dt(a), a.stride(0), _ptr(c), _ptr(b_q_weight), b_q_weight.numel(),
         _ptr(b_bias), _numel(b_bias), _ptr(b_scales), _dt(b_scales), b_scales.numel(),
         b_scales.shape[0], _numel(a_scales), _ptr(global_scale), _numel(global_scale),
-        _ptr(zeros), _dt(zeros), _numel(zeros), _numel(g_idx), _numel(perm), None, 0, b_type_id,
-        size_m, size_n, size_k, 1, 0, 0, int(is_zp_float), _stream()))
+        _ptr(zeros), _dt(zeros), _numel(zeros), _ptr(g_idx), _numel(g_idx), _ptr(perm),
+        _numel(perm), None, 0, b_type_id, size_m, size_n, size_k, int(is_k_full), 0, 0,
+        int(is_zp_float), _stream()))
     return c
 
 

@@ -71,6 +71,45 @@ hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, in
 }
 
 // ---------------------------------------------------------------------------------------
+// Act-order activation gather (upstream gptq_marlin's permute_cols step): the weights were
+// repacked with perm = argsort(g_idx), so their row j is source row perm[j]; A's columns are
+// gathered the same way and the GEMM then runs on contiguous groups.  g_idx is the sorted
+// one the layer passes (marlin_sort_g_idx: g_idx[perm]), so row j's group is g_idx[j], and
+// the grouped kernels need it to be j / group_size: every group holds exactly group_size
+// rows, as GPTQ's act-order quantizer forms them.  A column j that breaks that, or whose
+// perm entry is outside [0, size_k), is written as NaN, so the result shows it without a
+// host synchronisation.  Workgroup x covers 256 consecutive columns j, workgroup y walks
+// rows.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void permute_cols_kernel(const uint16_t* __restrict__ a,
+                                                           int64_t lda, const int* __restrict__ perm,
+                                                           const int* __restrict__ g_idx,
+                                                           int group_shift, int size_k, int64_t rows,
+                                                           uint16_t nan_bits,
+                                                           uint16_t* __restrict__ out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= size_k) return;
+  const int src = perm[j];
+  bool ok = src >= 0 && src < size_k;
+  if (group_shift >= 0) ok = ok && g_idx[j] == (j >> group_shift);
+  for (int64_t m = blockIdx.y; m < rows; m += gridDim.y)
+    out[m * size_k + j] = ok ? a[m * lda + src] : nan_bits;
+}
+
+hipError_t launch_permute_cols(const void* a, bool bf16, int64_t lda, const int* perm,
+                               const int* g_idx, int group_shift, int64_t size_k, int64_t size_m,
+                               void* out, hipStream_t stream) {
+  if (size_k == 0 || size_m == 0) return hipSuccess;
+  const unsigned gx = (unsigned)((size_k + 255) / 256);
+  const unsigned gy = (unsigned)std::min<int64_t>(size_m, 1024);
+  hipLaunchKernelGGL(permute_cols_kernel, dim3(gx, gy), dim3(256), 0, stream,
+                     reinterpret_cast<const uint16_t*>(a), lda, perm, g_idx, group_shift,
+                     (int)size_k, size_m, (uint16_t)(bf16 ? 0x7fc0u : 0x7e00u),
+                     reinterpret_cast<uint16_t*>(out));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
 // moe_align_block_size (reference moe_align_sum_kernels.cu:81-181, 291-320), one workgroup
 // of 1024 threads.  Unlike the reference's atomic scatter, placement is deterministic:
 // route indices of one expert appear in ascending order.

@@ -167,6 +167,32 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
   return w;
 }
 
+// Act-order staging buffer for A[:, perm], one per (device, stream), grown like the
+// workspace (refused while the stream captures a graph).  The gather kernel rewrites it in
+// full on every call, so it needs no clearing.
+void* get_act_order_buffer(int dev, hipStream_t stream, size_t elems) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+  std::lock_guard<std::mutex> lk(mu);
+  auto& b = bufs[{dev, stream}];
+  if (elems > b.second) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    check_hip(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
+    check_supported(cs == hipStreamCaptureStatusNone,
+                    "act_order staging buffer for this shape is not yet allocated on the "
+                    "capturing stream: run the same shape once on that stream before capturing");
+    const size_t n = std::max<size_t>(elems, std::max<size_t>(2 * b.second, size_t(1) << 20));
+    if (b.first) {
+      check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      check_hip(hipFree(b.first), "hipFree");
+      b = {nullptr, 0};
+    }
+    check_hip(hipMalloc(&b.first, n * sizeof(uint16_t)), "hipMalloc(act_order staging)");
+    b.second = n;
+  }
+  return b.first;
+}
+
 // ---- static split-K scratch of marlin_gemm_no_alloc -------------------------------------
 // One array per GPU, held until the process ends: kScratchPartials fp32 partial sums, then
 // kScratchCounters arrival counters.  A static __device__ array starts zeroed when the code
@@ -542,6 +568,7 @@ struct MetaCheck {
   int group_size;  // -1 channelwise
   int gsm;
   int group_shift;
+  int zp_packed;  // uint4/uint8 zero points are integer codes packed along N
 };
 
 MetaCheck check_weight_meta(int64_t b_type_id, marlin_dtype_t a_dtype,
@@ -584,20 +611,30 @@ MetaCheck check_weight_meta(int64_t b_type_id, marlin_dtype_t a_dtype,
   check(!has_zp || mc.fmt == FMT_U4 || mc.fmt == FMT_U8,
         "zero-point metadata is supported only for uint4 and uint8 weights.");
   if (has_zp) {
-    check(is_zp_float,
-          "received b_zeros but is_zp_float is false. Packed integer zero-points are not "
-          "supported on the uint4/uint8 path.");
     check(b_zeros != nullptr, "b_zeros pointer is null");
-    check(zeros_dtype == a_dtype,
-          "uint4/uint8 zero points must have the activation dtype (float16 or bfloat16).");
-    check(zeros_numel == scales_numel, "b_zeros numel = ", zeros_numel,
-          " is not num_groups * size_n = ", scales_numel / per_expert);
+    if (is_zp_float) {
+      check(zeros_dtype == a_dtype,
+            "uint4/uint8 float zero points must have the activation dtype (float16 or "
+            "bfloat16).");
+      check(zeros_numel == scales_numel, "b_zeros numel = ", zeros_numel,
+            " is not num_groups * size_n = ", scales_numel / per_expert);
+    } else {
+      // integer zero points packed along N, 32/bits per int32 word (upstream marlin's
+      // is_zp_float=false mode; the SM70 reference rejects it, marlin.cu:336-339)
+      const int64_t zpack = 32 / fmt_bits(mc.fmt);
+      check(zeros_dtype == MARLIN_DTYPE_INT32,
+            "packed integer zero points (is_zp_float=false) must be int32.");
+      check(size_n % zpack == 0, "size_n must be divisible by the zero-point pack factor");
+      check(zeros_numel * zpack == scales_numel, "b_zeros numel = ", zeros_numel,
+            " is not num_groups * size_n / pack_factor = ", scales_numel / zpack / per_expert);
+      mc.zp_packed = 1;
+    }
   } else {
     check(!is_zp_float, "is_zp_float is true but b_zeros was not provided.");
   }
   if (mc.fmt == FMT_U4 || mc.fmt == FMT_U8) {
-    check(has_zp && is_zp_float, mc.fmt == FMT_U4 ? "uint4" : "uint8",
-          " path requires float zero points (is_zp_float=true).");
+    check(has_zp, mc.fmt == FMT_U4 ? "uint4" : "uint8",
+          " path requires zero points (float with is_zp_float=true, or packed int32).");
   }
 
   // group-size support per format (reference marlin.cu:434-493, sm70_marlin_gemm.cuh:98-141)
@@ -706,6 +743,11 @@ struct DenseCall {
   GemmParams params;
   size_t ws_elems;     // fp32 partial sums (splits > 1)
   size_t ws_counters;  // arrival counters (splits > 1)
+  // act-order: A's columns are gathered by perm into a staging buffer first
+  bool act_order;
+  const int* perm;
+  const int* g_idx;
+  int act_group_shift;  // log2(group size), -1 channelwise
 };
 
 // Validation of marlin_gemm (reference marlin.cu:83-506) and everything the launch needs
@@ -715,11 +757,20 @@ DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_strid
                       int64_t b_bias_numel, const void* b_scales, marlin_dtype_t b_scales_dtype,
                       int64_t b_scales_numel, int64_t num_groups, int64_t a_scales_numel,
                       const float* global_scale, int64_t global_scale_numel, const void* b_zeros,
-                      marlin_dtype_t b_zeros_dtype, int64_t b_zeros_numel, int64_t g_idx_numel,
-                      int64_t perm_numel, int64_t b_type_id, int64_t size_m, int64_t size_n,
-                      int64_t size_k, int is_zp_float) {
-  check(g_idx_numel == 0, "marlin_gemm does not support act_order g_idx.");
-  check(perm_numel == 0, "marlin_gemm does not support act_order perm.");
+                      marlin_dtype_t b_zeros_dtype, int64_t b_zeros_numel, const int32_t* g_idx,
+                      int64_t g_idx_numel, const int32_t* perm, int64_t perm_numel,
+                      int64_t b_type_id, int64_t size_m, int64_t size_n, int64_t size_k,
+                      int is_zp_float, int is_k_full) {
+  const bool act_order = g_idx_numel > 0 || perm_numel > 0;
+  if (act_order) {
+    // act-order (upstream gptq_marlin; the SM70 reference rejects it, marlin.cu:95-102):
+    // weights repacked with perm = argsort(g_idx), A gathered by perm before the GEMM
+    check(g_idx_numel == size_k && perm_numel == size_k, "act_order needs g_idx and perm with "
+          "size_k = ", size_k, " entries each (got ", g_idx_numel, " and ", perm_numel, ")");
+    check(g_idx != nullptr && perm != nullptr, "null g_idx / perm pointer");
+    check_supported(is_k_full, "act_order with is_k_full=false (a row-parallel K shard) is not "
+                               "supported on this build");
+  }
   check_supported(is_half_type(a_dtype),
                   "only float16 and bfloat16 activations are supported (8-bit activations are "
                   "not implemented).");
@@ -728,6 +779,10 @@ DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_strid
                                          num_groups, 1, global_scale, global_scale_numel, 1,
                                          b_zeros, b_zeros_dtype, b_zeros_numel, is_zp_float,
                                          size_n, size_k);
+  if (act_order)
+    check_supported(mc.fmt == FMT_U4B8 || mc.fmt == FMT_U4 || mc.fmt == FMT_U8B128 ||
+                        mc.fmt == FMT_U8,
+                    "act_order is supported for integer weight types only");
   const int bits = fmt_bits(mc.fmt);
   const int64_t pack = 32 / bits;
   check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_size = ", 16);
@@ -742,6 +797,10 @@ DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_strid
   check(size_m >= 0 && size_m <= INT32_MAX, "size_m out of range");
   DenseCall d{};
   d.empty = size_m == 0 || size_n == 0;
+  d.act_order = act_order;
+  d.perm = perm;
+  d.g_idx = g_idx;
+  d.act_group_shift = mc.group_size > 0 ? mc.group_shift : -1;
   if (d.empty) return d;
   check(size_k > 0, "size_k must be positive");
   check(a && c && b_q_weight && b_scales, "null tensor pointer");
@@ -758,6 +817,7 @@ DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_strid
   p.b_expert_stride = 0;
   p.scales = b_scales;
   p.zeros = b_zeros_numel ? b_zeros : nullptr;
+  p.zp_packed = mc.zp_packed;
   p.meta_expert_stride = 0;
   p.bias = b_bias_numel ? b_bias : nullptr;
   p.global_scale = global_scale;
@@ -850,14 +910,13 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
                             int64_t a_scales_numel,
                             const float* global_scale, int64_t global_scale_numel,
                             const void* b_zeros, marlin_dtype_t b_zeros_dtype,
-                            int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel,
-                            void* workspace, int64_t workspace_bytes, int64_t b_type_id,
-                            int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
-                            int use_atomic_add, int use_fp32_reduce, int is_zp_float,
-                            marlin_stream_t stream) {
+                            int64_t b_zeros_numel, const int32_t* g_idx, int64_t g_idx_numel,
+                            const int32_t* perm, int64_t perm_numel, void* workspace,
+                            int64_t workspace_bytes, int64_t b_type_id, int64_t size_m,
+                            int64_t size_n, int64_t size_k, int is_k_full, int use_atomic_add,
+                            int use_fp32_reduce, int is_zp_float, marlin_stream_t stream) {
   (void)workspace;
   (void)workspace_bytes;
-  (void)is_k_full;
   (void)use_atomic_add;
   (void)use_fp32_reduce;
   return guarded([&] {
@@ -865,11 +924,21 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
                                     b_bias, b_bias_numel, b_scales, b_scales_dtype,
                                     b_scales_numel, num_groups, a_scales_numel, global_scale,
                                     global_scale_numel, b_zeros, b_zeros_dtype, b_zeros_numel,
-                                    g_idx_numel, perm_numel, b_type_id, size_m, size_n, size_k,
-                                    is_zp_float);
+                                    g_idx, g_idx_numel, perm, perm_numel, b_type_id, size_m,
+                                    size_n, size_k, is_zp_float, is_k_full);
     if (d.empty) return;
     hipStream_t s = (hipStream_t)stream;
     GemmParams p = d.params;
+    if (d.act_order) {
+      // A[:, perm] into a staging buffer (rows of size_k), then the plain grouped GEMM: the
+      // repacked weights' row j is source row perm[j], whose group is j / group_size
+      void* staged = get_act_order_buffer(d.dev, s, (size_t)size_m * size_k);
+      check_hip(launch_permute_cols(a, a_dtype == MARLIN_DTYPE_BFLOAT16, a_row_stride, d.perm,
+                                    d.g_idx, d.act_group_shift, size_k, size_m, staged, s),
+                "act_order permute launch");
+      p.a = staged;
+      p.a_stride = size_k;
+    }
     if (d.plan.plan.splits > 1) {
       Workspace& w = get_workspace(d.dev, s, d.ws_elems, d.ws_counters);
       p.ws = w.ws;
@@ -891,12 +960,15 @@ marlin_status_t marlin_gemm_no_alloc(const void* a, marlin_dtype_t a_dtype, int6
                                      int64_t size_m, int64_t size_n, int64_t size_k,
                                      int is_zp_float, marlin_stream_t stream) {
   return guarded([&] {
+    check_supported(g_idx_numel == 0 && perm_numel == 0,
+                    "marlin_gemm_no_alloc does not support act_order (its A staging buffer "
+                    "would need an allocation); use marlin_gemm");
     const DenseCall d = check_dense(a, a_dtype, a_row_stride, c, b_q_weight, b_q_weight_numel,
                                     b_bias, b_bias_numel, b_scales, b_scales_dtype,
                                     b_scales_numel, num_groups, a_scales_numel, global_scale,
                                     global_scale_numel, b_zeros, b_zeros_dtype, b_zeros_numel,
-                                    g_idx_numel, perm_numel, b_type_id, size_m, size_n, size_k,
-                                    is_zp_float);
+                                    nullptr, 0, nullptr, 0, b_type_id, size_m, size_n, size_k,
+                                    is_zp_float, 1);
     if (d.empty) return;
     hipStream_t s = (hipStream_t)stream;
     uint32_t* base = scratch_on_device(d.dev, s);
@@ -1047,6 +1119,7 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     p.b_expert_stride = size_k * size_n / pack;
     p.scales = b_scales;
     p.zeros = b_zeros_numel ? b_zeros : nullptr;
+    p.zp_packed = mc.zp_packed;
     p.meta_expert_stride = num_groups * size_n;
     p.bias = b_bias_numel ? b_bias : nullptr;
     p.global_scale = global_scale;
@@ -1135,7 +1208,8 @@ marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_
     const MetaCheck mc = check_weight_meta(b_type_id, out_dtype, b_scales_dtype, b_scales_numel,
                                            num_groups, 1, global_scale, global_scale_numel, 1,
                                            b_zeros, b_zeros_dtype, b_zeros_numel,
-                                           b_zeros_numel > 0 ? 1 : 0, size_n, size_k);
+                                           b_zeros_numel > 0 && b_zeros_dtype != MARLIN_DTYPE_INT32,
+                                           size_n, size_k);
     const int64_t pack = 32 / fmt_bits(mc.fmt);
     check(size_k % 32 == 0, "size_k must be divisible by 32");
     check(size_n % 16 == 0, "size_n must be divisible by 16");
@@ -1145,6 +1219,7 @@ marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_
     p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
     p.scales = b_scales;
     p.zeros = b_zeros_numel ? b_zeros : nullptr;
+    p.zp_packed = mc.zp_packed;
     p.global_scale = global_scale;
     p.alpha_exp = 7 - (out_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
     p.N = (int)size_n;

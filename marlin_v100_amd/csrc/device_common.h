@@ -150,6 +150,18 @@ struct MetaRaw {
   uint32_t z;
 };
 
+// MetaRaw::z holds an integer zero-point code (in its low bits) instead of the 16-bit float
+// zero point when this bit is set.
+constexpr uint32_t kIntZeroFlag = 0x80000000u;
+
+// Zero point z*s as fp32 for uint4/uint8: the float zero point as stored, or an integer code
+// times the scale (exact: <= 8 + 11 significant bits), so that the dequant below yields the
+// single rounding of the exact (q - z) * s.
+template <class AT>
+__device__ __forceinline__ float zero_point_value(uint32_t z, float s) {
+  return (z & kIntZeroFlag) ? (float)(z & 0xffu) * s : raw16_to_float(z & 0xffff, AT{});
+}
+
 template <int FMT, class AT>
 __device__ __forceinline__ Meta make_meta(MetaRaw raw) {
   Meta m;
@@ -186,7 +198,7 @@ __device__ __forceinline__ Meta make_meta(MetaRaw raw) {
       m.c1 = -1152.0f * s;  // (1024 + q)*s - 1152 s = (q - 128) s
       m.c16 = 0.f;
     } else {
-      const float z = raw16_to_float(raw.z & 0xffff, AT{});
+      const float z = zero_point_value<AT>(raw.z, s);
       m.c1 = __builtin_fmaf(-1024.0f, s, -z);  // exact: |1024 s + z| has <= 22 bits
       m.c16 = __builtin_fmaf(-64.0f, s, -z);
     }
@@ -373,7 +385,7 @@ __device__ __forceinline__ IMeta make_imeta(MetaRaw raw) {
   } else if constexpr (FMT == FMT_U8B128) {
     return IMeta{s, s * (IO::kMagic + 128.0f)};
   } else {
-    const float z = raw16_to_float(raw.z & 0xffff, AT{});
+    const float z = zero_point_value<AT>(raw.z, s);
     return IMeta{s, __builtin_fmaf(s, IO::kMagic, z)};
   }
 }

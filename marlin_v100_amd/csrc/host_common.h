@@ -20,6 +20,11 @@ hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, in
 hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, int bs, int* sorted,
                             int64_t sorted_numel, int* expert_ids, int64_t expert_ids_numel,
                             int* post_pad, const int* expert_map, hipStream_t stream);
+// act-order: out[m, j] = a[m, perm[j]] (rows of size_k), NaN where perm[j] is out of range
+// or, with grouped scales (group_shift >= 0), where the sorted g_idx[j] != j >> group_shift.
+hipError_t launch_permute_cols(const void* a, bool bf16, int64_t lda, const int* perm,
+                               const int* g_idx, int group_shift, int64_t size_k, int64_t size_m,
+                               void* out, hipStream_t stream);
 hipError_t launch_silu_and_mul(const void* x, bool bf16, int64_t rows, int64_t d, void* out,
                                hipStream_t stream);
 // kind: 0 fp16, 1 bf16, 2 fp32

@@ -159,10 +159,24 @@ at::Tensor op_marlin_gemm(at::Tensor& a, std::optional<at::Tensor> c_or_none, at
   if (b_zeros_or_none.has_value() && b_zeros_or_none->size(-1) > 0) {
     TORCH_CHECK(b_zeros_or_none->dim() == 2, "b_zeros rank = ", b_zeros_or_none->dim(),
                 " is not 2");
-    TORCH_CHECK(b_zeros_or_none->size(1) == size_n, "b_zeros dim 1 = ",
-                b_zeros_or_none->size(1), " is not size_n = ", size_n);
+    // float zero points [G, N]; packed integer zero points [G, N / pack_factor] int32
+    // (ScalarType id: exponent | mantissa << 8 | signed << 16 ..., vllm/scalar_type.py:25-43)
+    const int64_t bits = (b_type_id & 0xff) + ((b_type_id >> 8) & 0xff) + ((b_type_id >> 16) & 1);
+    const int64_t zn = is_zp_float ? size_n : size_n / (32 / std::max<int64_t>(bits, 1));
+    TORCH_CHECK(b_zeros_or_none->size(1) == zn, "b_zeros dim 1 = ", b_zeros_or_none->size(1),
+                " is not ", is_zp_float ? "size_n = " : "size_n / pack_factor = ", zn);
     TORCH_CHECK(b_zeros_or_none->size(0) == b_scales.size(0), "b_zeros dim 0 = ",
                 b_zeros_or_none->size(0), " is not num_groups = ", b_scales.size(0));
+  }
+  check_cuda_contig(g_idx_or_none, "g_idx");
+  check_cuda_contig(perm_or_none, "perm");
+  const bool act = (g_idx_or_none.has_value() && g_idx_or_none->numel() > 0) ||
+                   (perm_or_none.has_value() && perm_or_none->numel() > 0);
+  if (act) {
+    TORCH_CHECK(g_idx_or_none.has_value() && g_idx_or_none->scalar_type() == at::kInt,
+                "g_idx must be int32");
+    TORCH_CHECK(perm_or_none.has_value() && perm_or_none->scalar_type() == at::kInt,
+                "perm must be int32");
   }
 
   const at::OptionalDeviceGuard guard(a.device());
@@ -191,7 +205,10 @@ at::Tensor op_marlin_gemm(at::Tensor& a, std::optional<at::Tensor> c_or_none, at
                       opt_numel(a_scales_or_none),
                       reinterpret_cast<const float*>(opt_ptr(global_scale_or_none)),
                       opt_numel(global_scale_or_none), opt_ptr(b_zeros_or_none),
-                      opt_dtype(b_zeros_or_none), zeros_numel, opt_numel(g_idx_or_none),
+                      opt_dtype(b_zeros_or_none), zeros_numel,
+                      reinterpret_cast<const int32_t*>(opt_ptr(g_idx_or_none)),
+                      opt_numel(g_idx_or_none),
+                      reinterpret_cast<const int32_t*>(opt_ptr(perm_or_none)),
                       opt_numel(perm_or_none), workspace.numel() ? workspace.data_ptr() : nullptr,
                       workspace.nbytes(), b_type_id, size_m, size_n, size_k, is_k_full,
                       use_atomic_add, use_fp32_reduce, is_zp_float, cur_stream(a)));

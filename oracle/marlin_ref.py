@@ -281,6 +281,80 @@ def dequant_int(q: torch.Tensor, scales: torch.Tensor, fmt: str, out_dtype: torc
     return (qf * s - _expand(zp_f.to(torch.float32), k)).to(out_dtype)
 
 
+def dequant_int_zero(q: torch.Tensor, scales: torch.Tensor, z: torch.Tensor,
+                     out_dtype: torch.dtype, g_idx: torch.Tensor | None = None) -> torch.Tensor:
+    """Integer zero points (upstream marlin's is_zp_float=False, marlin_utils.py:347-396):
+    dtype((q - z) * s), one rounding of the exact value (the reference rejects this mode,
+    marlin.cu:336-339).  g_idx: per-row group index instead of row // group_size."""
+    k = q.shape[0]
+    if g_idx is None:
+        s, zz = _expand(scales.to(torch.float32), k), _expand(z.to(torch.float32), k)
+    else:
+        s, zz = scales.to(torch.float32)[g_idx.long()], z.to(torch.float32)[g_idx.long()]
+    return ((q.to(torch.float32) - zz) * s).to(out_dtype)
+
+
+def dequant_int_g_idx(q: torch.Tensor, scales: torch.Tensor, fmt: str, out_dtype: torch.dtype,
+                      g_idx: torch.Tensor, zp_f: torch.Tensor | None = None) -> torch.Tensor:
+    """dequant_int with act-order groups: row k uses scale row g_idx[k]
+    (upstream gptq act-order; tests/helpers.py:1122-1133 semantics per row)."""
+    gi = g_idx.long()
+    s = scales.to(torch.float32)[gi]
+    qf = q.to(torch.float32)
+    if fmt in ("u4b8", "u8b128"):
+        bias = 8.0 if fmt == "u4b8" else 128.0
+        return ((qf - bias) * s).to(out_dtype)
+    return (qf * s - zp_f.to(torch.float32)[gi]).to(out_dtype)
+
+
+def act_order_groups(k: int, gs: int, gen: torch.Generator):
+    """A GPTQ act-order grouping: a random column order `perm` (GPTQ's descending-activation
+    order) and g_idx[perm[j]] = j // gs, so each group holds gs rows and argsort(g_idx)
+    returns those groups contiguously (marlin_utils.py:274-276)."""
+    perm = torch.randperm(k, generator=gen)
+    g_idx = torch.empty(k, dtype=torch.int32)
+    g_idx[perm] = (torch.arange(k) // gs).to(torch.int32)
+    return g_idx
+
+
+def quantize_g_idx(w: torch.Tensor, g_idx: torch.Tensor, num_groups: int, fmt: str,
+                   dtype: torch.dtype):
+    """RTN with act-order groups: the group of row k is g_idx[k].  Returns (q [K, N] codes,
+    s [G, N], z [G, N] int or None, zp_f [G, N] or None) with the formulas of
+    quantize_with_bias / quantize_with_zero_point applied per group's row set."""
+    k, n = w.shape
+    bits = 4 if fmt in ("u4b8", "u4") else 8
+    q = torch.empty((k, n), dtype=torch.int32)
+    ss, zs, zfs = [], [], []
+    for g in range(num_groups):
+        rows = (g_idx == g).nonzero().flatten()
+        if fmt in ("u4b8", "u8b128"):
+            qg, sg = quantize_with_bias(w[rows], -1, 8 if fmt == "u4b8" else 128, dtype)
+            zg = zfg = None
+        else:
+            qg, sg, zg, zfg = quantize_with_zero_point(w[rows], -1, bits, dtype)
+        q[rows] = qg
+        ss.append(sg)
+        zs.append(zg)
+        zfs.append(zfg)
+    s = torch.cat(ss)
+    if fmt in ("u4b8", "u8b128"):
+        return q, s, None, None
+    return q, s, torch.cat(zs), torch.cat(zfs)
+
+
+def pack_cols(z: torch.Tensor, bits: int) -> torch.Tensor:
+    """Codes [G, N] packed along N, 32/bits per int32, column n in bits [bits*(n % pack), ...)
+    (quant_utils.py:66-78)."""
+    g, n = z.shape
+    pack = 32 // bits
+    zz = z.to(torch.int64).reshape(g, n // pack, pack)
+    out = torch.zeros((g, n // pack), dtype=torch.int64)
+    for i in range(pack):
+        out |= zz[:, :, i] << (bits * i)
+    return _to_i32(out)
+
+
 def dequant_mxfp4(q: torch.Tensor, scales_e8m0: torch.Tensor, out_dtype: torch.dtype):
     """dtype(e2m1 * 2^(e-127)) (tests/helpers.py:1164-1184)."""
     k = q.shape[0]

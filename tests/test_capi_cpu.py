@@ -34,30 +34,40 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert capi.load().marlin_abi_version() == 1
+    assert capi.load().marlin_abi_version() == 2
 
 
 def _gemm(**kw):
     args = dict(a=16, a_dtype=capi.F16, a_row_stride=256, c=16, bq=16, bq_numel=256 * 512 // 8,
                 bias=None, bias_numel=0, scales=16, scales_dtype=capi.F16, scales_numel=2 * 512,
                 groups=2, a_scales_numel=0, glob=None, glob_numel=0, zeros=None,
-                zeros_dtype=capi.F16, zeros_numel=0, gidx=0, perm=0, type_id=TYPE_ID["u4b8"],
-                m=4, n=512, k=256, zp_float=0)
+                zeros_dtype=capi.F16, zeros_numel=0, gidx_ptr=None, gidx=0, perm_ptr=None, perm=0,
+                type_id=TYPE_ID["u4b8"], m=4, n=512, k=256, zp_float=0, k_full=1)
     args.update(kw)
     lib = capi.load()
     st = lib.marlin_gemm(args["a"], args["a_dtype"], args["a_row_stride"], args["c"], args["bq"],
                          args["bq_numel"], args["bias"], args["bias_numel"], args["scales"],
                          args["scales_dtype"], args["scales_numel"], args["groups"],
                          args["a_scales_numel"], args["glob"], args["glob_numel"], args["zeros"],
-                         args["zeros_dtype"], args["zeros_numel"], args["gidx"], args["perm"],
-                         None, 0, args["type_id"], args["m"], args["n"], args["k"], 1, 0, 0,
-                         args["zp_float"], None)
+                         args["zeros_dtype"], args["zeros_numel"], args["gidx_ptr"], args["gidx"],
+                         args["perm_ptr"], args["perm"], None, 0, args["type_id"], args["m"],
+                         args["n"], args["k"], args["k_full"], 0, 0, args["zp_float"], None)
     return st, lib.marlin_get_last_error().decode()
 
 
 @pytest.mark.parametrize("kw,status,msg", [
-    (dict(gidx=4), capi.STATUS_INVALID, "act_order g_idx"),
-    (dict(perm=4), capi.STATUS_INVALID, "act_order perm"),
+    (dict(gidx=4), capi.STATUS_INVALID, "act_order needs g_idx and perm"),
+    (dict(perm=256, perm_ptr=16), capi.STATUS_INVALID, "act_order needs g_idx and perm"),
+    (dict(gidx=256, perm=256), capi.STATUS_INVALID, "null g_idx / perm"),
+    (dict(gidx=256, perm=256, gidx_ptr=16, perm_ptr=16, k_full=0), capi.STATUS_NOT_SUPPORTED,
+     "is_k_full=false"),
+    (dict(gidx=256, perm=256, gidx_ptr=16, perm_ptr=16, type_id=TYPE_ID["fp8"],
+          scales_dtype=capi.F16, groups=1, scales_numel=512), capi.STATUS_NOT_SUPPORTED,
+     "integer weight types"),
+    (dict(type_id=TYPE_ID["u4"], zeros=16, zeros_numel=2 * 512 // 8, zeros_dtype=capi.F16),
+     capi.STATUS_INVALID, "must be int32"),
+    (dict(type_id=TYPE_ID["u4"], zeros=16, zeros_numel=2 * 512, zeros_dtype=capi.I32),
+     capi.STATUS_INVALID, "num_groups * size_n / pack_factor"),
     (dict(a_dtype=capi.F32), capi.STATUS_NOT_SUPPORTED, "float16 and bfloat16"),
     (dict(type_id=12345), capi.STATUS_NOT_SUPPORTED, "implements only"),
     (dict(n=96, scales_numel=2 * 96, bq_numel=256 * 96 // 8), capi.STATUS_INVALID,
@@ -65,7 +75,7 @@ def _gemm(**kw):
     (dict(k=240, a_row_stride=240, scales_numel=512, groups=1, bq_numel=240 * 512 // 8),
      capi.STATUS_INVALID, "size_k % 32 == 0"),
     (dict(zeros=16, zeros_numel=2 * 512, zp_float=1), capi.STATUS_INVALID, "zero-point"),
-    (dict(type_id=TYPE_ID["u4"]), capi.STATUS_INVALID, "float zero points"),
+    (dict(type_id=TYPE_ID["u4"]), capi.STATUS_INVALID, "requires zero points"),
     (dict(zp_float=1), capi.STATUS_INVALID, "is_zp_float is true but b_zeros"),
     (dict(groups=3, scales_numel=3 * 512), capi.STATUS_INVALID, "not divisible by b_scales"),
     (dict(groups=16, scales_numel=16 * 512), capi.STATUS_INVALID, "unsupported group_size"),
@@ -85,6 +95,15 @@ def test_gemm_rejections(kw, status, msg):
     st, err = _gemm(**kw)
     assert st == status, err
     assert msg in err, err
+
+
+def test_no_alloc_rejects_act_order():
+    lib = capi.load()
+    st = lib.marlin_gemm_no_alloc(16, capi.F16, 256, 16, 16, 256 * 256 // 8, None, 0, 16,
+                                  capi.F16, 2 * 256, 2, 0, None, 0, None, capi.F16, 0, 256, 256,
+                                  TYPE_ID["u4b8"], 2, 256, 256, 0, None)
+    assert st == capi.STATUS_NOT_SUPPORTED
+    assert "act_order" in lib.marlin_get_last_error().decode()
 
 
 def test_gemm_m_zero_is_noop():
@@ -118,7 +137,7 @@ def test_moe_rejections():
     st, err = call(bs=128)
     assert st == 1 and "unsupported moe_block_size=128" in err
     st, err = call(zeros_numel=0, zp=0)
-    assert st == 1 and "float zero points" in err
+    assert st == 1 and "requires zero points" in err
 
 
 def test_moe_align_rejections():

@@ -456,3 +456,99 @@ def test_planted_grouped_topk_top1_group_score_is_caught():
     assert top2 == [1, 0] and top1 == [1, 2]
     _, ids = O.grouped_topk(x[None, :], 3, 2, 3, True, 1.0, np.zeros(6, np.float32), 0)
     assert sorted({i // 2 for i in ids[0].tolist()}) == sorted(top2)
+
+
+# ---- integer zero points and act-order (upstream modes the SM70 reference rejects) --------
+
+def test_dequant_int_zero_brute_force():
+    """Every (code, zero) pair against (q - z) * s computed exactly in float64 and rounded once."""
+    for dtype in (torch.float16, torch.bfloat16):
+        q = torch.arange(16, dtype=torch.int32).repeat_interleave(16).reshape(256, 1)
+        z = torch.arange(16, dtype=torch.int32).repeat(16).reshape(256, 1)
+        s = torch.tensor([[0.0123]], dtype=dtype)
+        # one group per row: expand through g_idx
+        g_idx = torch.arange(256)
+        zz = z.reshape(256, 1)
+        ss = s.repeat(256, 1)
+        got = O.dequant_int_zero(q, ss, zz, dtype, g_idx=g_idx)
+        exact = ((q.double() - z.double()) * s.double()).to(dtype)
+        assert torch.equal(got.view(torch.int16), exact.view(torch.int16))
+
+
+def test_dequant_int_zero_agrees_with_float_zero_when_exact():
+    """When z * s is representable in the dtype, the float-zero-point path (reference
+    semantics, tests/helpers.py:1576-1641) gives the same single rounding."""
+    gen = torch.Generator().manual_seed(1)
+    k, n = 256, 64
+    q = torch.randint(0, 16, (k, n), generator=gen, dtype=torch.int32)
+    z = torch.randint(0, 16, (2, n), generator=gen, dtype=torch.int32)
+    s = (2.0 ** -torch.randint(3, 9, (2, n), generator=gen)).to(torch.bfloat16)  # powers of two
+    zp_f = (z.float() * s.float()).to(torch.bfloat16)
+    assert torch.equal(zp_f.float(), z.float() * s.float())
+    a = O.dequant_int_zero(q, s, z, torch.bfloat16)
+    b = O.dequant_int(q, s, "u4", torch.bfloat16, zp_f)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_planted_zero_point_sign_is_caught():
+    """A slip that adds the zero point instead of subtracting it fails the brute force."""
+    q = torch.tensor([[3]], dtype=torch.int32)
+    z = torch.tensor([[5]], dtype=torch.int32)
+    s = torch.tensor([[0.5]], dtype=torch.float16)
+    good = O.dequant_int_zero(q, s, z, torch.float16)
+    assert good.item() == -1.0
+    slipped = ((q.float() + z.float()) * s.float()).half()
+    assert slipped.item() != good.item()
+
+
+def test_pack_cols_closed_form():
+    """Word j of row g holds codes of columns pack*j .. pack*j+pack-1, LSB first
+    (quant_utils.py:66-78), brute-forced on arange codes."""
+    for bits in (4, 8):
+        pack = 32 // bits
+        z = (torch.arange(2 * 64) % (1 << bits)).reshape(2, 64).to(torch.int32)
+        w = O.pack_cols(z, bits)
+        assert w.shape == (2, 64 // pack)
+        for g in range(2):
+            for j in range(64 // pack):
+                exp = sum(int(z[g, pack * j + i]) << (bits * i) for i in range(pack))
+                assert (int(w[g, j]) & 0xffffffff) == exp
+
+
+def test_act_order_groups_sort_to_contiguous_groups():
+    gen = torch.Generator().manual_seed(2)
+    g_idx = O.act_order_groups(512, 64, gen)
+    order = torch.argsort(g_idx)
+    assert torch.equal(g_idx[order], (torch.arange(512) // 64).to(torch.int32))
+    assert torch.equal(torch.bincount(g_idx.long()), torch.full((8,), 64))
+
+
+def test_dequant_g_idx_is_a_row_permutation_of_grouped_dequant():
+    """Permuting the rows of a contiguously grouped weight (and its g_idx with them) permutes
+    the dequant: links dequant_int_g_idx to the pinned dequant_int."""
+    gen = torch.Generator().manual_seed(3)
+    k, n, gs = 256, 32, 64
+    w = torch.randn((k, n), generator=gen) * 0.02
+    for fmt in ("u4b8", "u4", "u8b128"):
+        if fmt == "u4":
+            q, s, _z, zp = O.quantize_with_zero_point(w, gs, 4, torch.float16)
+        else:
+            q, s = O.quantize_with_bias(w, gs, 8 if fmt == "u4b8" else 128, torch.float16)
+            zp = None
+        base = O.dequant_int(q, s, fmt, torch.float16, zp)
+        perm = torch.randperm(k, generator=gen)
+        g_idx = (torch.arange(k) // gs)[perm]
+        got = O.dequant_int_g_idx(q[perm], s, fmt, torch.float16, g_idx, zp)
+        assert torch.equal(got, base[perm])
+
+
+def test_quantize_g_idx_reconstruction_bound():
+    gen = torch.Generator().manual_seed(4)
+    k, n, gs = 512, 64, 128
+    g_idx = O.act_order_groups(k, gs, gen)
+    w = torch.randn((k, n), generator=gen) * 0.02
+    for fmt in ("u4b8", "u4", "u8b128"):
+        q, s, z, zp = O.quantize_g_idx(w, g_idx, k // gs, fmt, torch.float32)
+        deq = O.dequant_int_g_idx(q, s, fmt, torch.float32, g_idx, zp)
+        err = (deq - w).abs()
+        assert (err <= s[g_idx.long()] * 0.5 + 1e-6).all(), fmt
