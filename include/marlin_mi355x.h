@@ -207,6 +207,31 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     int64_t thread_n, int64_t blocks_per_sm, marlin_stream_t stream);
 
 /*
+ * MoE stage 1 with the SiLU-gated activation fused: the arguments of
+ * marlin_moe_wna16_marlin_gemm (size_n = 2 * I, the gate columns first), but c receives
+ * silu(h[:, :I]) * h[:, I:] as [size_m * top_k, size_n / 2] instead of h, rounded as
+ * marlin_moe_wna16_marlin_gemm followed by marlin_silu_and_mul round it.  No counterpart op
+ * in the reference: it fuses the reference's stage 1 and activation
+ * (fused_marlin_moe.py:183-212, activation.py:45-52).  Only the multistage kernel's plans
+ * are fused (larger batches, size_n % 256 == 0, no split K); for any other plan it returns
+ * MARLIN_STATUS_NOT_SUPPORTED before launching anything, and the caller runs the two passes.
+ */
+marlin_status_t marlin_moe_wna16_marlin_gemm_silu(
+    const void* a, marlin_dtype_t a_dtype, void* c, const int32_t* b_q_weight,
+    int64_t b_q_weight_numel, int64_t num_experts, const void* b_bias, int64_t b_bias_numel,
+    const void* b_scales, marlin_dtype_t b_scales_dtype, int64_t b_scales_numel,
+    int64_t num_groups, int64_t a_scales_numel, const float* global_scale,
+    int64_t global_scale_numel, const void* b_zeros, marlin_dtype_t b_zeros_dtype,
+    int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel, void* workspace,
+    int64_t workspace_bytes, const int32_t* sorted_token_ids, int64_t sorted_numel,
+    const int32_t* expert_ids, int64_t expert_ids_numel,
+    const int32_t* num_tokens_past_padded, const float* topk_weights,
+    int64_t topk_weights_numel, int64_t moe_block_size, int64_t top_k, int mul_topk_weights,
+    int64_t b_type_id, int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,
+    int use_atomic_add, int use_fp32_reduce, int is_zp_float, int64_t thread_k,
+    int64_t thread_n, int64_t blocks_per_sm, marlin_stream_t stream);
+
+/*
  * Dequantize repacked weights to [size_k, size_n] (row-major) in out_dtype (fp16 or bf16),
  * with the device dequant routines the GEMM uses.  Test and inspection aid, no counterpart
  * op in the reference: it restates the reference's dequant helpers

@@ -37,7 +37,7 @@ HIP_FLAGS = [
 
 # (the GEMM instance files take longest: they go to the compile pool first)
 HIP_SOURCES = [f"gemm_{fmt}_{at}.hip" for fmt in ("u4", "u4b8", "u8", "u8b128", "fp8", "mxfp4",
-                                                  "nvfp4") for at in ("bf16", "f16")] + [
+                                                  "nvfp4", "u4z", "u8z") for at in ("bf16", "f16")] + [
     "capi.hip",
     "repack.hip",
     "aux_kernels.hip",

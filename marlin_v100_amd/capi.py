@@ -50,6 +50,11 @@ SIGNATURES = {
                                           _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I,
                                           _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I64, _I64,
                                           _I64, _P]),
+    "marlin_moe_wna16_marlin_gemm_silu": (_I, [_P, _I, _P, _P, _I64, _I64, _P, _I64, _P, _I,
+                                               _I64, _I64, _I64, _P, _I64, _P, _I, _I64, _I64,
+                                               _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64,
+                                               _I64, _I64, _I, _I64, _I64, _I64, _I64, _I, _I, _I,
+                                               _I, _I64, _I64, _I64, _P]),
     "marlin_dequantize": (_I, [_P, _I64, _P, _I, _I64, _I64, _P, _I, _I64, _P, _I64, _I64, _I64,
                                _I64, _I, _P, _P]),
     "marlin_moe_sum": (_I, [_P, _I, _I64, _I64, _I64, _P, _P]),
@@ -171,11 +176,16 @@ def moe_align_block_size(topk_ids, num_experts, block_size, sorted_token_ids, ex
 def moe_wna16_marlin_gemm(a, b_q_weight, b_scales, sorted_token_ids, expert_ids,
                           num_tokens_past_padded, topk_weights, moe_block_size, top_k,
                           mul_topk_weights, b_type_id, size_m, size_n, size_k, *, c=None,
-                          b_bias=None, global_scale=None, b_zeros=None, is_zp_float=False):
+                          b_bias=None, global_scale=None, b_zeros=None, is_zp_float=False,
+                          silu_gated=False):
+    """silu_gated: the fused stage-1 entry (c gets silu(h[:, :N/2]) * h[:, N/2:]); raises
+    MarlinError with STATUS_NOT_SUPPORTED when the plan cannot fuse it."""
+    out_n = size_n // 2 if silu_gated else size_n
     if c is None:
-        c = torch.empty((size_m * top_k, size_n), dtype=a.dtype, device=a.device)
+        c = torch.empty((size_m * top_k, out_n), dtype=a.dtype, device=a.device)
     zeros = b_zeros if (b_zeros is not None and b_zeros.numel()) else None
-    _check(load().marlin_moe_wna16_marlin_gemm(
+    fn = load().marlin_moe_wna16_marlin_gemm_silu if silu_gated else load().marlin_moe_wna16_marlin_gemm
+    _check(fn(
         _ptr(a), _dt(a), _ptr(c), _ptr(b_q_weight), b_q_weight.numel(), b_q_weight.shape[0],
         _ptr(b_bias), _numel(b_bias), _ptr(b_scales), _dt(b_scales), b_scales.numel(),
         b_scales.shape[1], 0, _ptr(global_scale), _numel(global_scale), _ptr(zeros), _dt(zeros),

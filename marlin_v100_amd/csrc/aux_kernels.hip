@@ -63,6 +63,8 @@ hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, in
     case FMT_U4: return launch_dequant_fmt<FMT_U4>(p, bf16, o, gs_mode, stream);
     case FMT_U8B128: return launch_dequant_fmt<FMT_U8B128>(p, bf16, o, gs_mode, stream);
     case FMT_U8: return launch_dequant_fmt<FMT_U8>(p, bf16, o, gs_mode, stream);
+    case FMT_U4Z: return launch_dequant_fmt<FMT_U4Z>(p, bf16, o, gs_mode, stream);
+    case FMT_U8Z: return launch_dequant_fmt<FMT_U8Z>(p, bf16, o, gs_mode, stream);
     case FMT_FP8: return launch_dequant_fmt<FMT_FP8>(p, bf16, o, gs_mode, stream);
     case FMT_MXFP4: return launch_dequant_fmt<FMT_MXFP4>(p, bf16, o, gs_mode, stream);
     case FMT_NVFP4: return launch_dequant_fmt<FMT_NVFP4>(p, bf16, o, gs_mode, stream);
@@ -105,6 +107,31 @@ hipError_t launch_permute_cols(const void* a, bool bf16, int64_t lda, const int*
   hipLaunchKernelGGL(permute_cols_kernel, dim3(gx, gy), dim3(256), 0, stream,
                      reinterpret_cast<const uint16_t*>(a), lda, perm, g_idx, group_shift,
                      (int)size_k, size_m, (uint16_t)(bf16 ? 0x7fc0u : 0x7e00u),
+                     reinterpret_cast<uint16_t*>(out));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
+// Packed integer zero points -> 16-bit codes: out[e] = code e of the int32 words, where
+// word e / pack holds codes e, e+1, ... from its low bits up (pack = 32 / bits).  The GEMM
+// kernels then read integer zero points with the same loads as float ones.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void expand_zeros_kernel(const uint32_t* __restrict__ words,
+                                                           int bits, int64_t n,
+                                                           uint16_t* __restrict__ out) {
+  const int pack = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x)
+    out[e] = (uint16_t)((words[e / pack] >> (bits * (int)(e % pack))) & mask);
+}
+
+hipError_t launch_expand_zeros(const void* words, int bits, int64_t n_codes, void* out,
+                               hipStream_t stream) {
+  if (n_codes == 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((n_codes + 255) / 256, 16384);
+  hipLaunchKernelGGL(expand_zeros_kernel, dim3(grid), dim3(256), 0, stream,
+                     reinterpret_cast<const uint32_t*>(words), bits, n_codes,
                      reinterpret_cast<uint16_t*>(out));
   return hipGetLastError();
 }
@@ -430,13 +457,6 @@ hipError_t launch_moe_sum(const void* in, int kind, int64_t tokens, int topk, in
 // silu_and_mul: out[r, j] = silu(x[r, j]) * x[r, d + j], rounded as the reference's torch
 // expression F.silu(gate) * up rounds: silu to the element type, then the product.
 // ---------------------------------------------------------------------------------------
-template <class AT>
-__device__ __forceinline__ float silu_mul1(uint32_t g_raw, uint32_t u_raw) {
-  const float g = raw16_to_float(g_raw & 0xffffu, AT{});
-  const float u = raw16_to_float(u_raw & 0xffffu, AT{});
-  const float s = raw16_to_float(to_raw16(g / (1.0f + expf(-g)), AT{}), AT{});
-  return s * u;
-}
 
 // d % 8 == 0: 8 outputs (16 bytes) per thread
 template <class AT>

@@ -167,30 +167,45 @@ Workspace& get_workspace(int dev, hipStream_t stream, size_t need_elems, size_t 
   return w;
 }
 
-// Act-order staging buffer for A[:, perm], one per (device, stream), grown like the
-// workspace (refused while the stream captures a graph).  The gather kernel rewrites it in
-// full on every call, so it needs no clearing.
-void* get_act_order_buffer(int dev, hipStream_t stream, size_t elems) {
+// Staging buffers, one per (purpose, device, stream), grown like the workspace (refused
+// while the stream captures a graph): the act-order copy of A[:, perm] and the 16-bit codes
+// of packed integer zero points.  Each call rewrites what it uses in full, so they need no
+// clearing.
+enum StagingSlot { kStageActOrder = 0, kStageZeros = 1 };
+void* get_staging(int slot, int dev, hipStream_t stream, size_t bytes) {
   static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+  static std::map<std::tuple<int, int, hipStream_t>, std::pair<void*, size_t>> bufs;
   std::lock_guard<std::mutex> lk(mu);
-  auto& b = bufs[{dev, stream}];
-  if (elems > b.second) {
+  auto& b = bufs[{slot, dev, stream}];
+  if (bytes > b.second) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     check_hip(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
     check_supported(cs == hipStreamCaptureStatusNone,
-                    "act_order staging buffer for this shape is not yet allocated on the "
-                    "capturing stream: run the same shape once on that stream before capturing");
-    const size_t n = std::max<size_t>(elems, std::max<size_t>(2 * b.second, size_t(1) << 20));
+                    slot == kStageActOrder
+                        ? "act_order staging buffer for this shape is not yet allocated on the "
+                          "capturing stream: run the same shape once on that stream before "
+                          "capturing"
+                        : "zero-point staging buffer for this shape is not yet allocated on the "
+                          "capturing stream: run the same shape once on that stream before "
+                          "capturing");
+    const size_t n = std::max<size_t>(bytes, std::max<size_t>(2 * b.second, size_t(1) << 21));
     if (b.first) {
       check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
       check_hip(hipFree(b.first), "hipFree");
       b = {nullptr, 0};
     }
-    check_hip(hipMalloc(&b.first, n * sizeof(uint16_t)), "hipMalloc(act_order staging)");
+    check_hip(hipMalloc(&b.first, n), "hipMalloc(staging)");
     b.second = n;
   }
   return b.first;
+}
+
+// Packed integer zero points -> 16-bit codes in a staging buffer; returns the codes.
+const void* stage_int_zeros(int dev, hipStream_t stream, const void* words, int bits,
+                            int64_t n_codes) {
+  void* codes = get_staging(kStageZeros, dev, stream, (size_t)n_codes * sizeof(uint16_t));
+  check_hip(launch_expand_zeros(words, bits, n_codes, codes, stream), "zero-point expand launch");
+  return codes;
 }
 
 // ---- static split-K scratch of marlin_gemm_no_alloc -------------------------------------
@@ -553,6 +568,8 @@ hipError_t dispatch_gemm(const GemmLaunch& l, const GemmParams& p, hipStream_t s
     MMI_CASE_FMT(FMT_U4, u4)
     MMI_CASE_FMT(FMT_U8B128, u8b128)
     MMI_CASE_FMT(FMT_U8, u8)
+    MMI_CASE_FMT(FMT_U4Z, u4z)
+    MMI_CASE_FMT(FMT_U8Z, u8z)
     MMI_CASE_FMT(FMT_FP8, fp8)
     MMI_CASE_FMT(FMT_MXFP4, mxfp4)
     MMI_CASE_FMT(FMT_NVFP4, nvfp4)
@@ -658,6 +675,8 @@ MetaCheck check_weight_meta(int64_t b_type_id, marlin_dtype_t a_dtype,
     mc.group_shift = ilog2_exact(group_size);
     mc.gsm = group_size >= 128 ? GSM_BIG : GSM_SMALL;
   }
+  // integer zero points run the integer-zero instances (the codes are staged as 16 bits)
+  if (mc.zp_packed) mc.fmt = mc.fmt == FMT_U4 ? FMT_U4Z : FMT_U8Z;
   return mc;
 }
 
@@ -781,7 +800,7 @@ DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_strid
                                          size_n, size_k);
   if (act_order)
     check_supported(mc.fmt == FMT_U4B8 || mc.fmt == FMT_U4 || mc.fmt == FMT_U8B128 ||
-                        mc.fmt == FMT_U8,
+                        mc.fmt == FMT_U8 || fmt_int_zero(mc.fmt),
                     "act_order is supported for integer weight types only");
   const int bits = fmt_bits(mc.fmt);
   const int64_t pack = 32 / bits;
@@ -817,7 +836,6 @@ DenseCall check_dense(const void* a, marlin_dtype_t a_dtype, int64_t a_row_strid
   p.b_expert_stride = 0;
   p.scales = b_scales;
   p.zeros = b_zeros_numel ? b_zeros : nullptr;
-  p.zp_packed = mc.zp_packed;
   p.meta_expert_stride = 0;
   p.bias = b_bias_numel ? b_bias : nullptr;
   p.global_scale = global_scale;
@@ -929,10 +947,13 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
     if (d.empty) return;
     hipStream_t s = (hipStream_t)stream;
     GemmParams p = d.params;
+    if (fmt_int_zero(d.plan.launch.fmt))
+      p.zeros = stage_int_zeros(d.dev, s, p.zeros, fmt_bits(d.plan.launch.fmt),
+                                (int64_t)num_groups * size_n);
     if (d.act_order) {
       // A[:, perm] into a staging buffer (rows of size_k), then the plain grouped GEMM: the
       // repacked weights' row j is source row perm[j], whose group is j / group_size
-      void* staged = get_act_order_buffer(d.dev, s, (size_t)size_m * size_k);
+      void* staged = get_staging(kStageActOrder, d.dev, s, (size_t)size_m * size_k * 2);
       check_hip(launch_permute_cols(a, a_dtype == MARLIN_DTYPE_BFLOAT16, a_row_stride, d.perm,
                                     d.g_idx, d.act_group_shift, size_k, size_m, staged, s),
                 "act_order permute launch");
@@ -970,6 +991,9 @@ marlin_status_t marlin_gemm_no_alloc(const void* a, marlin_dtype_t a_dtype, int6
                                     nullptr, 0, nullptr, 0, b_type_id, size_m, size_n, size_k,
                                     is_zp_float, 1);
     if (d.empty) return;
+    check_supported(!fmt_int_zero(d.plan.launch.fmt),
+                    "marlin_gemm_no_alloc does not support packed integer zero points (their "
+                    "16-bit staging would need an allocation); use marlin_gemm");
     hipStream_t s = (hipStream_t)stream;
     uint32_t* base = scratch_on_device(d.dev, s);
     GemmParams p = d.params;
@@ -1022,7 +1046,8 @@ marlin_status_t marlin_moe_align_block_size(const void* topk_ids, marlin_dtype_t
   });
 }
 
-marlin_status_t marlin_moe_wna16_marlin_gemm(
+static marlin_status_t moe_gemm(bool gated,
+    
     const void* a, marlin_dtype_t a_dtype, void* c, const int32_t* b_q_weight,
     int64_t b_q_weight_numel, int64_t num_experts, const void* b_bias, int64_t b_bias_numel,
     const void* b_scales, marlin_dtype_t b_scales_dtype, int64_t b_scales_numel,
@@ -1119,7 +1144,6 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
     p.b_expert_stride = size_k * size_n / pack;
     p.scales = b_scales;
     p.zeros = b_zeros_numel ? b_zeros : nullptr;
-    p.zp_packed = mc.zp_packed;
     p.meta_expert_stride = num_groups * size_n;
     p.bias = b_bias_numel ? b_bias : nullptr;
     p.global_scale = global_scale;
@@ -1187,13 +1211,60 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
       l.occ = 1;
       l.grid = (unsigned)((int64_t)m_blocks * groups);
     }
+    if (gated) {
+      // the fused activation runs in the multistage kernel's epilogue; any other plan (the
+      // few-routes decode kernel, a split K, narrower column blocks, the tiled kernel) is
+      // reported as NOT_SUPPORTED before anything launches, and the caller runs the two
+      // passes instead
+      check_supported(l.stream && l.depth == 0 && nt == 4 && splits == 1 && size_n % 256 == 0 &&
+                          !ov.any,
+                      "the fused SiLU stage-1 epilogue does not cover this shape or batch");
+      l.gated = true;
+      check_supported(instantiated(l), "no gated moe kernel instance for this configuration");
+    }
     if (ov.any && !instantiated(l))
       check_supported(false, "no moe kernel instance for the selected configuration; a "
                              "MARLIN_MI355X_* tuning override selects a configuration this "
                              "build does not instantiate");
+    if (fmt_int_zero(mc.fmt))
+      p.zeros = stage_int_zeros(dev, s, b_zeros, fmt_bits(mc.fmt),
+                                num_experts * num_groups * size_n);
     check_hip(dispatch_gemm(l, p, s), "moe_wna16_marlin_gemm launch");
   });
 }
+
+#define MMI_MOE_ARGS_DECL                                                                        \
+    const void* a, marlin_dtype_t a_dtype, void* c, const int32_t* b_q_weight,                  \
+    int64_t b_q_weight_numel, int64_t num_experts, const void* b_bias, int64_t b_bias_numel,    \
+    const void* b_scales, marlin_dtype_t b_scales_dtype, int64_t b_scales_numel,                \
+    int64_t num_groups, int64_t a_scales_numel, const float* global_scale,                      \
+    int64_t global_scale_numel, const void* b_zeros, marlin_dtype_t b_zeros_dtype,              \
+    int64_t b_zeros_numel, int64_t g_idx_numel, int64_t perm_numel, void* workspace,            \
+    int64_t workspace_bytes, const int32_t* sorted_token_ids, int64_t sorted_numel,             \
+    const int32_t* expert_ids, int64_t expert_ids_numel,                                        \
+    const int32_t* num_tokens_past_padded, const float* topk_weights,                           \
+    int64_t topk_weights_numel, int64_t moe_block_size, int64_t top_k, int mul_topk_weights,    \
+    int64_t b_type_id, int64_t size_m, int64_t size_n, int64_t size_k, int is_k_full,           \
+    int use_atomic_add, int use_fp32_reduce, int is_zp_float, int64_t thread_k,                 \
+    int64_t thread_n, int64_t blocks_per_sm, marlin_stream_t stream
+#define MMI_MOE_ARGS                                                                             \
+    a, a_dtype, c, b_q_weight, b_q_weight_numel, num_experts, b_bias, b_bias_numel, b_scales,     \
+    b_scales_dtype, b_scales_numel, num_groups, a_scales_numel, global_scale, global_scale_numel, \
+    b_zeros, b_zeros_dtype, b_zeros_numel, g_idx_numel, perm_numel, workspace, workspace_bytes,   \
+    sorted_token_ids, sorted_numel, expert_ids, expert_ids_numel, num_tokens_past_padded,         \
+    topk_weights, topk_weights_numel, moe_block_size, top_k, mul_topk_weights, b_type_id, size_m, \
+    size_n, size_k, is_k_full, use_atomic_add, use_fp32_reduce, is_zp_float, thread_k, thread_n,  \
+    blocks_per_sm, stream
+
+marlin_status_t marlin_moe_wna16_marlin_gemm(MMI_MOE_ARGS_DECL) {
+  return moe_gemm(false, MMI_MOE_ARGS);
+}
+
+marlin_status_t marlin_moe_wna16_marlin_gemm_silu(MMI_MOE_ARGS_DECL) {
+  return moe_gemm(true, MMI_MOE_ARGS);
+}
+#undef MMI_MOE_ARGS_DECL
+#undef MMI_MOE_ARGS
 
 marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_numel,
                                   const void* b_scales, marlin_dtype_t b_scales_dtype,
@@ -1219,12 +1290,17 @@ marlin_status_t marlin_dequantize(const int32_t* b_q_weight, int64_t b_q_weight_
     p.b = reinterpret_cast<const uint32_t*>(b_q_weight);
     p.scales = b_scales;
     p.zeros = b_zeros_numel ? b_zeros : nullptr;
-    p.zp_packed = mc.zp_packed;
     p.global_scale = global_scale;
     p.alpha_exp = 7 - (out_dtype == MARLIN_DTYPE_FLOAT16 ? 14 : 126);
     p.N = (int)size_n;
     p.K = (int)size_k;
     p.group_shift = mc.group_shift;
+    if (fmt_int_zero(mc.fmt)) {
+      int dev = 0;
+      check_hip(hipGetDevice(&dev), "hipGetDevice");
+      p.zeros = stage_int_zeros(dev, (hipStream_t)stream, b_zeros, fmt_bits(mc.fmt),
+                                num_groups * size_n);
+    }
     check_hip(launch_dequant(mc.fmt, p, out_dtype == MARLIN_DTYPE_BFLOAT16, out, mc.gsm,
                              (hipStream_t)stream),
               "marlin_dequantize launch");

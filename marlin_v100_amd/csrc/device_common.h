@@ -52,12 +52,17 @@ enum Fmt : int {
   FMT_FP8 = 4,    // float8_e4m3fn, scales carry the x256 exponent fold
   FMT_MXFP4 = 5,  // float4_e2m1f + float8_e8m0fnu scale per 32
   FMT_NVFP4 = 6,  // float4_e2m1f + S0E5M3 scale per 16 + fp32 global scale
+  FMT_U4Z = 7,    // uint4 + integer zero point (16-bit codes expanded by the launcher)
+  FMT_U8Z = 8,    // uint8 + integer zero point
 };
 
 __host__ __device__ constexpr int fmt_bits(int f) {
-  return (f == FMT_U8B128 || f == FMT_U8 || f == FMT_FP8) ? 8 : 4;
+  return (f == FMT_U8B128 || f == FMT_U8 || f == FMT_U8Z || f == FMT_FP8) ? 8 : 4;
 }
-__host__ __device__ constexpr bool fmt_has_zp(int f) { return f == FMT_U4 || f == FMT_U8; }
+__host__ __device__ constexpr bool fmt_int_zero(int f) { return f == FMT_U4Z || f == FMT_U8Z; }
+__host__ __device__ constexpr bool fmt_has_zp(int f) {
+  return f == FMT_U4 || f == FMT_U8 || fmt_int_zero(f);
+}
 __host__ __device__ constexpr bool fmt_byte_scale(int f) {
   return f == FMT_MXFP4 || f == FMT_NVFP4;
 }
@@ -150,16 +155,13 @@ struct MetaRaw {
   uint32_t z;
 };
 
-// MetaRaw::z holds an integer zero-point code (in its low bits) instead of the 16-bit float
-// zero point when this bit is set.
-constexpr uint32_t kIntZeroFlag = 0x80000000u;
-
-// Zero point z*s as fp32 for uint4/uint8: the float zero point as stored, or an integer code
-// times the scale (exact: <= 8 + 11 significant bits), so that the dequant below yields the
-// single rounding of the exact (q - z) * s.
-template <class AT>
+// Zero point z*s as fp32 for uint4/uint8: the float zero point as stored, or (integer-zero
+// formats) the code times the scale (exact: <= 8 + 11 significant bits), so that the dequant
+// below yields the single rounding of the exact (q - z) * s.
+template <int FMT, class AT>
 __device__ __forceinline__ float zero_point_value(uint32_t z, float s) {
-  return (z & kIntZeroFlag) ? (float)(z & 0xffu) * s : raw16_to_float(z & 0xffff, AT{});
+  if constexpr (fmt_int_zero(FMT)) return (float)(z & 0xffu) * s;
+  else return raw16_to_float(z & 0xffff, AT{});
 }
 
 template <int FMT, class AT>
@@ -198,7 +200,7 @@ __device__ __forceinline__ Meta make_meta(MetaRaw raw) {
       m.c1 = -1152.0f * s;  // (1024 + q)*s - 1152 s = (q - 128) s
       m.c16 = 0.f;
     } else {
-      const float z = zero_point_value<AT>(raw.z, s);
+      const float z = zero_point_value<FMT, AT>(raw.z, s);
       m.c1 = __builtin_fmaf(-1024.0f, s, -z);  // exact: |1024 s + z| has <= 22 bits
       m.c16 = __builtin_fmaf(-64.0f, s, -z);
     }
@@ -244,7 +246,7 @@ template <int FMT, class AT>
 __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, const Meta& m,
                                                  uint32_t vz) {
   u32x4_t r;
-  if constexpr (FMT == FMT_U4B8 || FMT == FMT_U4) {
+  if constexpr (FMT == FMT_U4B8 || FMT == FMT_U4 || FMT == FMT_U4Z) {
     const uint32_t x0 = and_or_halves<0x000f000fu>(w0, 0x64006400u, vz);  // k0, k4  : 1024 + q
     const uint32_t x1 = and_or_halves<0x00f000f0u>(w0, 0x64006400u, vz);  // k1, k5  : 1024 + 16q
     const uint32_t t = w0 >> 8;
@@ -262,7 +264,7 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
     r[1] = pack2(e2, e3, AT{});
     r[2] = pack2(e4, e5, AT{});
     r[3] = pack2(e6, e7, AT{});
-  } else if constexpr (FMT == FMT_U8B128 || FMT == FMT_U8) {
+  } else if constexpr (FMT == FMT_U8B128 || FMT == FMT_U8 || FMT == FMT_U8Z) {
     const uint32_t a0 = and_or_halves<0x00ff00ffu>(w0, 0x64006400u, vz);       // k0, k2
     const uint32_t a1 = and_or_halves<0x00ff00ffu>(w0 >> 8, 0x64006400u, vz);  // k1, k3
     const uint32_t b0 = and_or_halves<0x00ff00ffu>(w1, 0x64006400u, vz);       // k4, k6
@@ -354,7 +356,7 @@ __device__ __forceinline__ u32x4_t dequant_operand(uint32_t w0, uint32_t w1, con
 template <int FMT, class AT>
 struct IntOperand {
   static constexpr bool kEnabled = FMT == FMT_U4B8 || FMT == FMT_U4 || FMT == FMT_U8B128 ||
-                                   FMT == FMT_U8 || FMT == FMT_FP8;
+                                   FMT == FMT_U8 || FMT == FMT_FP8 || fmt_int_zero(FMT);
   // fp16 with a fixed code offset (uint4b8, uint8b128): one v_pk_add_f16 per register turns
   // 1024+q into the signed value q-bias exactly, so the group sums need no row-sum term
   static constexpr bool kDirect = AT::kId == 0 && (FMT == FMT_U4B8 || FMT == FMT_U8B128);
@@ -385,7 +387,7 @@ __device__ __forceinline__ IMeta make_imeta(MetaRaw raw) {
   } else if constexpr (FMT == FMT_U8B128) {
     return IMeta{s, s * (IO::kMagic + 128.0f)};
   } else {
-    const float z = zero_point_value<AT>(raw.z, s);
+    const float z = zero_point_value<FMT, AT>(raw.z, s);
     return IMeta{s, __builtin_fmaf(s, IO::kMagic, z)};
   }
 }
@@ -482,6 +484,18 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, f3
                                           BF16) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// silu(g) * u on 16-bit inputs, rounded as the reference's torch expression
+// F.silu(gate) * up rounds (activation.py:45-52): silu to the element type, then the product
+// (the caller rounds it).  Shared by silu_and_mul and the gated MoE epilogue, so the fused
+// and the two-pass paths give the same bits.
+template <class AT>
+__device__ __forceinline__ float silu_mul1(uint32_t g_raw, uint32_t u_raw) {
+  const float g = raw16_to_float(g_raw & 0xffffu, AT{});
+  const float u = raw16_to_float(u_raw & 0xffffu, AT{});
+  const float s = raw16_to_float(to_raw16(g / (1.0f + expf(-g)), AT{}), AT{});
+  return s * u;
 }
 
 // Logical column -> storage index of a bias permuted with marlin_permute_bias

@@ -25,6 +25,7 @@ static hipError_t launch_or_query(const GemmLaunch& l, Kernel kernel, unsigned t
 
 template <int FMT, class AT, int GSM>
 static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
+  if (l.gated && (l.depth > 0 || !l.stream)) return hipErrorInvalidValue;  // multistage only
   if (l.depth > 0) {
 #define MMI_DECODE(NT_, D_, WPB_, KS_, MOE_, OCC_)                                           \
   if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_ && l.moe == MOE_ &&       \
@@ -57,9 +58,20 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
 // budget: those stay on marlin_gemm_kernel)
 #define MMI_STREAM(BM_, NT_, MOE_)                                                          \
   if constexpr (!(GSM == GSM_SMALL && BM_ >= 48 && NT_ >= 4)) {                             \
-    if (l.bm == BM_ && l.nt == NT_ && l.moe == MOE_)                                        \
+    if (l.bm == BM_ && l.nt == NT_ && l.moe == MOE_ && !l.gated)                            \
       return launch_or_query(l, marlin_stream_kernel<FMT, AT, BM_, NT_, GSM, MOE_>, 256, p, s); \
   }
+// MoE stage 1 with the gated activation fused
+#define MMI_STREAM_GATED(BM_)                                                                \
+  if constexpr (!(GSM == GSM_SMALL && BM_ >= 48)) {                                          \
+    if (l.bm == BM_ && l.nt == 4 && l.moe && l.gated)                                        \
+      return launch_or_query(l, marlin_stream_kernel<FMT, AT, BM_, 4, GSM, true, true>, 256, p, s); \
+  }
+    MMI_STREAM_GATED(16)
+    MMI_STREAM_GATED(32)
+    MMI_STREAM_GATED(48)
+    MMI_STREAM_GATED(64)
+#undef MMI_STREAM_GATED
     MMI_STREAM(16, 1, false)
     MMI_STREAM(16, 2, false)
     MMI_STREAM(16, 4, false)

@@ -62,8 +62,6 @@ struct GemmParams {
   int mul_topk;
   int valid_ids;  // size_m * top_k
   int zero;       // always 0: source of an opaque VGPR zero (opaque_zero())
-  int zp_packed;  // uint4/uint8: zeros are integer codes packed along N (32/bits per int32
-                  // word, column n in bits [bits*(n % pack), ...)), not float zero points
 };
 
 // Group-size modes.
@@ -88,16 +86,11 @@ __device__ __forceinline__ MetaRaw load_meta_raw(const GemmParams& p, int64_t ba
   } else if constexpr (FMT == FMT_MXFP4) {
     return MetaRaw{reinterpret_cast<const uint8_t*>(p.scales)[idx + col], 0u};
   } else if constexpr (fmt_has_zp(FMT)) {
-    uint32_t z;
-    if (p.zp_packed) {
-      // integer code, flagged with bit 31 for make_meta / make_imeta
-      constexpr int ZB = fmt_bits(FMT), ZP = 32 / ZB;
-      const uint32_t w = reinterpret_cast<const uint32_t*>(p.zeros)[(idx + col) / ZP];
-      z = ((w >> (ZB * (col % ZP))) & ((1u << ZB) - 1u)) | kIntZeroFlag;
-    } else {
-      z = load_u16<AT>(p.zeros, idx + col);
-    }
-    return MetaRaw{load_u16<AT>(p.scales, idx + col), z};
+    // a float zero point, or (integer-zero formats) the 16-bit code the launcher expanded
+    // from the caller's packed int32 words into the same [G, N] layout
+    const int64_t e = idx + col;
+    const uint32_t z = load_u16<AT>(p.zeros, e);
+    return MetaRaw{load_u16<AT>(p.scales, e), z};
   } else {
     return MetaRaw{load_u16<AT>(p.scales, idx + col), 0u};
   }

@@ -1,0 +1,5 @@
+// gemm_u4z_bf16.hip -- GEMM kernel instances for u4 weights with integer zero points and bf16 activations.
+#define MMI_FMT mmi::FMT_U4Z
+#define MMI_AT mmi::BF16
+#define MMI_FN launch_gemm_u4z_bf16
+#include "gemm_instances.h"

@@ -25,6 +25,9 @@ hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, i
 hipError_t launch_permute_cols(const void* a, bool bf16, int64_t lda, const int* perm,
                                const int* g_idx, int group_shift, int64_t size_k, int64_t size_m,
                                void* out, hipStream_t stream);
+// packed integer zero points (int32 words, 32/bits codes each) -> 16-bit codes
+hipError_t launch_expand_zeros(const void* words, int bits, int64_t n_codes, void* out,
+                               hipStream_t stream);
 hipError_t launch_silu_and_mul(const void* x, bool bf16, int64_t rows, int64_t d, void* out,
                                hipStream_t stream);
 // kind: 0 fp16, 1 bf16, 2 fp32
@@ -58,6 +61,7 @@ struct GemmLaunch {
   int occ;      // decode kernel: waves per SIMD its registers must allow (1: compiler's choice)
   bool stream;  // multistage kernel for 16..64-row blocks (bm, nt, moe; ch unused)
   bool moe;
+  bool gated;   // multistage MoE stage 1 with the SiLU-gated activation fused (nt 4)
   unsigned grid;
   int* occupancy;  // when set: report workgroups per CU instead of launching
   int* scratch;    // with occupancy: also report the kernel's scratch bytes per lane
@@ -74,6 +78,8 @@ MMI_DECLARE_LAUNCH(u8)
 MMI_DECLARE_LAUNCH(fp8)
 MMI_DECLARE_LAUNCH(mxfp4)
 MMI_DECLARE_LAUNCH(nvfp4)
+MMI_DECLARE_LAUNCH(u4z)
+MMI_DECLARE_LAUNCH(u8z)
 #undef MMI_DECLARE_LAUNCH
 
 }  // namespace mmi

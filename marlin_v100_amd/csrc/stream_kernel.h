@@ -30,7 +30,13 @@
 
 namespace mmi {
 
-template <int FMT, class AT, int BM, int NT, int GSM, bool MOE>
+// GATED (MoE stage 1 with the SiLU-gated activation fused, splits == 1, 16x16 form): the
+// workgroup's column block is 128 gate columns and the 128 matching up columns N/2 later;
+// waves 0-1 stream the gate tiles and waves 2-3 the up tiles (4 KiB contiguous per step each,
+// as in the plain kernel).  The up waves pass their finished, rounded outputs to the gate
+// waves through LDS, which store silu(gate) * up into the [rows, N/2] output with the same
+// rounding as the two-pass path (stage-1 output, then silu_and_mul).
+template <int FMT, class AT, int BM, int NT, int GSM, bool MOE, bool GATED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM >= 128 ? 1 : 2, 8)))
 void marlin_stream_kernel(const GemmParams p) {
   constexpr int MT = BM / 16;
@@ -132,7 +138,9 @@ void marlin_stream_kernel(const GemmParams p) {
     }
   };
 
-  const int tn0 = n_blk * (BN / 16) + wave * NT;
+  static_assert(!GATED || (MOE && !M32), "gated epilogue: MoE blocks, 16x16 form");
+  const int tn0 = GATED ? (wave < 2 ? 0 : (p.N >> 5)) + n_blk * (BN / 32) + (wave & 1) * NT
+                        : n_blk * (BN / 16) + wave * NT;
   const int64_t chunk_stride = (int64_t)(p.N >> 4) * 256;
   const uint32_t* bptr = p.b + (int64_t)expert * p.b_expert_stride + (int64_t)tn0 * 256 + lane * 4;
   const int64_t meta_base = (int64_t)expert * p.meta_expert_stride;
@@ -511,6 +519,61 @@ void marlin_stream_kernel(const GemmParams p) {
           for (int e = 0; e < 4; ++e) f(i * 16 + lg * 4 + e, (tn0 + t) * 16 + ln, acc[i][t][e]);
     }
   };
+
+  if constexpr (GATED) {
+    // value of one output as the two-pass path stores it (finish() without the store)
+    auto stage1_value = [&](int64_t orow, int col, float v) __attribute__((always_inline)) {
+      float o = v * alpha;
+      if (bias != nullptr) {
+        float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
+                                  AT{});
+        if (p.mul_topk) bv *= alpha;
+        o += bv;
+      }
+      if (p.mul_topk) o *= p.topk_w[orow];
+      return (uint32_t)to_raw16(o, AT{});
+    };
+    // Gate wave w and up wave w + 2 hold the two factors of the same outputs.  Each finishes
+    // half of them: the gate wave the first half (it receives those up values), the up wave
+    // the second half (it receives those gate values), so the SiLU work is spread over all
+    // four waves.
+    constexpr int PER = MT * NT * 4;  // outputs per lane
+    constexpr int HALF = PER / 2;
+    uint16_t* xch = reinterpret_cast<uint16_t*>(lds_a0);  // [2 pairs][PER][64]
+    static_assert(2 * PER * 64 * 2 <= (int)sizeof(lds_a0), "exchange fits the staging buffer");
+    const bool up = wave >= 2;
+    uint16_t* mine = xch + (wave & 1) * PER * 64;  // this pair's exchange area
+    __syncthreads();  // every wave is done reading the staging buffers
+    {
+      int j = 0;
+      for_out([&](int r, int col, float v) __attribute__((always_inline)) {
+        // the gate wave hands over its second half, the up wave its first half
+        if (up ? j < HALF : j >= HALF) {
+          const int64_t orow = out_row(r);
+          mine[j * 64 + lane] = orow >= 0 ? (uint16_t)stage1_value(orow, col, v) : 0;
+        }
+        ++j;
+      });
+    }
+    __syncthreads();
+    {
+      const int half = p.N >> 1;
+      int j = 0;
+      for_out([&](int r, int col, float v) __attribute__((always_inline)) {
+        const bool own = up ? j >= HALF : j < HALF;
+        const int jj = j++;
+        if (!own) return;
+        const int64_t orow = out_row(r);
+        if (orow < 0) return;
+        const uint32_t other = mine[jj * 64 + lane];
+        const uint32_t self = stage1_value(orow, col, v);
+        const uint32_t g = up ? other : self;
+        const uint32_t u = up ? self : other;
+        cout[orow * half + (up ? col - half : col)] = to_raw16(silu_mul1<AT>(g, u), AT{});
+      });
+    }
+    return;
+  }
 
   if (p.splits == 1) {
     for_out([&](int r, int col, float v) __attribute__((always_inline)) { finish(r, col, v); });

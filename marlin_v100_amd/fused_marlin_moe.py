@@ -102,6 +102,26 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
     capi.silu_and_mul(out, x.contiguous())
 
 
+def _stage1_silu_fused(x, out, w1, bias1, w1_scale, global_scale1, w1_zeros, sorted_token_ids,
+                       expert_ids, num_tokens_post_padded, topk_weights, block_size_m, topk,
+                       mul_topk, quant_type, size_m, size_n, size_k, is_zp_float) -> bool:
+    """Stage 1 with the gated SiLU fused (marlin_moe_wna16_marlin_gemm_silu).  False when the
+    library's plan for this batch cannot fuse it (nothing was launched then)."""
+    from . import capi
+
+    try:
+        capi.moe_wna16_marlin_gemm(
+            x, w1, w1_scale, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights,
+            block_size_m, topk, mul_topk, quant_type.id, size_m, size_n, size_k, c=out,
+            b_bias=bias1, global_scale=global_scale1, b_zeros=w1_zeros,
+            is_zp_float=is_zp_float, silu_gated=True)
+    except capi.MarlinError as err:
+        if err.status == capi.STATUS_NOT_SUPPORTED:
+            return False
+        raise
+    return True
+
+
 def _unsupported(name: str, t) -> bool:
     return t is not None and (not isinstance(t, torch.Tensor) or t.numel() > 0)
 
@@ -130,10 +150,14 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
                      intermediate_cache2: torch.Tensor | None = None,
                      is_k_full: bool = True, output: torch.Tensor | None = None,
                      input_dtype: torch.dtype | None = None, inplace: bool = False, *,
-                     block_size_m: int | None = None) -> torch.Tensor:
-    """The reference's fused_marlin_moe (fused_marlin_moe.py:217-382).  `block_size_m`
-    (keyword only, not in the reference) fixes the moe block size instead of the
-    reference's heuristic."""
+                     block_size_m: int | None = None,
+                     fuse_activation: bool = False) -> torch.Tensor:
+    """The reference's fused_marlin_moe (fused_marlin_moe.py:217-382).  Keyword-only
+    extensions (not in the reference): `block_size_m` fixes the moe block size instead of the
+    reference's heuristic; `fuse_activation` runs stage 1 with the SiLU-gated activation in
+    its epilogue where the library's plan allows it (same bits as the two passes).  It is off
+    by default: on the BASELINE cfg5 shape the fused stage-1 kernel measured slower than stage
+    1 plus the activation pass (T = 2048: 661 against 608 + 29 us per kernel)."""
     if inplace:
         assert output is None, "Conflicting request"
     if isinstance(activation, str):
@@ -185,16 +209,27 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     cache3 = intermediate_cache13.flatten()[: m * topk * k].view(m * topk, k)
     cache2 = intermediate_cache2.flatten()[: m * topk * n].view(m * topk, n)
 
-    cache1 = ops.moe_wna16_marlin_gemm(
-        hidden_states, cache1, w1, bias1, w1_scale, None, global_scale1, w1_zeros, None, None,
-        workspace, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights,
-        moe_block_size=block_size_m, top_k=topk, mul_topk_weights=apply_router_weight_on_input,
-        b_q_type=quant_type, size_m=m, size_n=shards * n, size_k=k, is_k_full=is_k_full,
-        use_atomic_add=False, use_fp32_reduce=True, is_zp_float=is_w1_zp_float)
-    if activation == MoEActivation.SILU and activation_func is apply_moe_activation:
-        silu_and_mul(cache2, cache1.view(-1, 2 * n))
-    else:
-        activation_func(activation, cache2, cache1.view(-1, shards * n))
+    default_silu = activation == MoEActivation.SILU and activation_func is apply_moe_activation
+    fused = False
+    if fuse_activation and default_silu and m * topk > 16 * e and (2 * n) % 256 == 0:
+        # stage 1 with silu(gate) * up in its epilogue: cache2 directly, no [T*topk, 2I]
+        # intermediate and no activation pass (same bits as the two passes below)
+        fused = _stage1_silu_fused(hidden_states, cache2, w1, bias1, w1_scale, global_scale1,
+                                   w1_zeros, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                                   topk_weights, block_size_m, topk, apply_router_weight_on_input,
+                                   quant_type, m, 2 * n, k, is_w1_zp_float)
+    if not fused:
+        cache1 = ops.moe_wna16_marlin_gemm(
+            hidden_states, cache1, w1, bias1, w1_scale, None, global_scale1, w1_zeros, None,
+            None, workspace, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights,
+            moe_block_size=block_size_m, top_k=topk,
+            mul_topk_weights=apply_router_weight_on_input, b_q_type=quant_type, size_m=m,
+            size_n=shards * n, size_k=k, is_k_full=is_k_full, use_atomic_add=False,
+            use_fp32_reduce=True, is_zp_float=is_w1_zp_float)
+        if default_silu:
+            silu_and_mul(cache2, cache1.view(-1, 2 * n))
+        else:
+            activation_func(activation, cache2, cache1.view(-1, shards * n))
     if expert_map is not None:
         cache3.zero_()
     out3 = ops.moe_wna16_marlin_gemm(

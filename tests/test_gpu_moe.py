@@ -330,3 +330,75 @@ def test_fused_marlin_moe_reference_keywords():
         fused_marlin_moe(x, w13, w2, None, None, s13, s2, tw, ids, tid,
                          g_idx1=torch.zeros(H, dtype=torch.int32, device="cuda"),
                          w1_zeros=z13, w2_zeros=z2, is_w1_zp_float=True, is_w2_zp_float=True)
+
+
+@pytest.mark.parametrize("fmt", ["u4", "u4b8", "u8b128", "nvfp4"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bs", [16, 32, 48, 64])
+@pytest.mark.parametrize("bias,mul", [(False, False), (True, True)])
+def test_moe_stage1_silu_fused_is_bit_exact(fmt, dtype, bs, bias, mul):
+    """marlin_moe_wna16_marlin_gemm_silu == marlin_moe_wna16_marlin_gemm then silu_and_mul,
+    bit for bit (the fused epilogue rounds the stage-1 outputs as the store would, then applies
+    the same silu_mul); the two-pass path itself is checked against the oracle above."""
+    E, T, topk, K, I = 4, 96, 2, 256, 256
+    if fmt == "nvfp4" and bs >= 48:
+        pytest.skip("small-group metadata of 48/64-row blocks takes the tiled kernel (not fused)")
+    print(f"case fused-silu fmt={fmt} dtype={dtype} bs={bs} bias={bias} mul={mul}", flush=True)
+    tid, words, scales, zeros, glob, _deq = _make_experts(fmt, E, K, 2 * I, dtype, 700 + bs)
+    gen = torch.Generator().manual_seed(bs)
+    x = torch.randn((T, K), generator=gen).to(dtype).cuda()
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    numel = ids.numel()
+    s = torch.empty(numel + E * (bs - 1), dtype=torch.int32, device="cuda")
+    e = torch.empty(s.numel() // bs + 1, dtype=torch.int32, device="cuda")
+    npad = torch.empty(1, dtype=torch.int32, device="cuda")
+    capi.moe_align_block_size(ids.cuda(), E, bs, s, e, npad)
+    b = (torch.randn((E, 2 * I), generator=gen) * 0.1).to(dtype).cuda() if bias else None
+    kw = dict(b_bias=b, global_scale=glob, b_zeros=zeros, is_zp_float=zeros is not None)
+    args = (x, words, scales, s, e, npad, tw.cuda(), bs, topk, mul, tid, T, 2 * I, K)
+    h = capi.moe_wna16_marlin_gemm(*args, **kw)
+    ref = torch.empty((T * topk, I), dtype=dtype, device="cuda")
+    capi.silu_and_mul(ref, h)
+    out = torch.full((T * topk, I), float("nan"), dtype=dtype, device="cuda")
+    capi.moe_wna16_marlin_gemm(*args, c=out, silu_gated=True, **kw)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_moe_stage1_silu_fused_declines_decode_batches():
+    """Few routes per expert take the decode kernel, which the fused entry does not cover:
+    it reports NOT_SUPPORTED and launches nothing (fused_marlin_moe then runs two passes)."""
+    E, T, topk, K, I, bs = 16, 8, 2, 256, 256, 16
+    tid, words, scales, zeros, _g, _d = _make_experts("u4", E, K, 2 * I, torch.bfloat16, 5)
+    ids = torch.randint(0, E, (T, topk), dtype=torch.int32)
+    s = torch.empty(ids.numel() + E * (bs - 1), dtype=torch.int32, device="cuda")
+    e = torch.empty(s.numel() // bs + 1, dtype=torch.int32, device="cuda")
+    npad = torch.empty(1, dtype=torch.int32, device="cuda")
+    capi.moe_align_block_size(ids.cuda(), E, bs, s, e, npad)
+    x = torch.randn((T, K)).bfloat16().cuda()
+    out = torch.full((T * topk, I), 7.0, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(capi.MarlinError) as err:
+        capi.moe_wna16_marlin_gemm(x, words, scales, s, e, npad, torch.ones(T * topk).cuda(), bs,
+                                   topk, False, tid, T, 2 * I, K, c=out, b_zeros=zeros,
+                                   is_zp_float=True, silu_gated=True)
+    assert err.value.status == capi.STATUS_NOT_SUPPORTED
+    torch.cuda.synchronize()
+    assert (out == 7.0).all()
+
+
+def test_fused_marlin_moe_fuse_activation_matches_two_pass():
+    """fused_marlin_moe(fuse_activation=True) gives the two-pass layer's bits (batch large
+    enough for the multistage kernel)."""
+    from marlin_v100_amd.fused_marlin_moe import fused_marlin_moe
+
+    T, E, topk, H, I = 200, 8, 2, 256, 128
+    dtype = torch.bfloat16
+    tid, w13, s13, z13, _, _d13 = _make_experts("u4", E, H, 2 * I, dtype, 90)
+    _, w2, s2, z2, _, _d2 = _make_experts("u4", E, I, H, dtype, 91)
+    gen = torch.Generator().manual_seed(92)
+    x = torch.randn((T, H), generator=gen).to(dtype).cuda()
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    kw = dict(w1_zeros=z13, w2_zeros=z2, is_w1_zp_float=True, is_w2_zp_float=True)
+    two = fused_marlin_moe(x, w13, w2, None, None, s13, s2, tw.cuda(), ids.cuda(), tid, **kw)
+    one = fused_marlin_moe(x, w13, w2, None, None, s13, s2, tw.cuda(), ids.cuda(), tid,
+                           fuse_activation=True, **kw)
+    assert torch.equal(one.view(torch.int16), two.view(torch.int16))
