@@ -135,8 +135,8 @@ marlin_status_t marlin_gemm(const void* a, marlin_dtype_t a_dtype, int64_t a_row
  * counters returns MARLIN_STATUS_INVALID_ARGUMENT.  The first call on a device clears the
  * array with one fill kernel on `stream`.  Every call on a GPU shares that GPU's array:
  * calls that overlap on one GPU (different streams, or host threads) race.  Act-order
- * (g_idx_numel or perm_numel non-zero) returns MARLIN_STATUS_NOT_SUPPORTED: its activation
- * staging buffer would need an allocation.
+ * (g_idx_numel or perm_numel non-zero) and packed integer zero points return
+ * MARLIN_STATUS_NOT_SUPPORTED: their staging buffers would need an allocation.
  */
 #define MARLIN_NO_ALLOC_MAX_PARTIALS 2097152
 #define MARLIN_NO_ALLOC_MAX_COUNTERS 65536
