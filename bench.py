@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy (counter calibration for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only run torch.matmul (hipBLASLt) at the large-M shapes, unquantized: "
+                         "the MFMA rate a vendor GEMM sustains on this part")
     return ap.parse_args()
 
 
@@ -57,6 +60,23 @@ def copy_probe(steps: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_read": src.numel() * 4,
                       "copy_probe_bytes_written": dst.numel() * 4, "launches": steps}))
+    return 0
+
+
+def gemm_probe(steps: int) -> int:
+    """torch.matmul (hipBLASLt) at the cfg3 and cfg2 M=1024 shapes with 16-bit weights: the
+    MFMA rate an unquantized vendor GEMM sustains here, beside the published peak."""
+    import torch
+
+    out = {}
+    for m, k, n, dt in ((4096, 8192, 8192, torch.float16), (1024, 5120, 34816, torch.bfloat16)):
+        a = torch.randn(m, k, device="cuda", dtype=dt)
+        b = torch.randn(k, n, device="cuda", dtype=dt)
+        t = time_calls([lambda: a @ b], steps, max(3, steps // 10))
+        out[f"{m}x{k}x{n}_{str(dt).replace('torch.', '')}"] = {
+            "us": round(t * 1e6, 2), "TFLOPs": round(2.0 * m * k * n / t / 1e12, 1),
+            "mfma_frac": round(2.0 * m * k * n / t / 1e12 / MFMA_PEAK_TFLOPS, 4)}
+    print(json.dumps({"gemm_probe": out}))
     return 0
 
 
@@ -398,6 +418,8 @@ def main() -> int:
         return 1
     if args.copy_probe:
         return copy_probe(args.steps)
+    if args.gemm_probe:
+        return gemm_probe(args.steps)
     from marlin_v100_amd import ops  # noqa: F401  (loads the native libraries; no fallback)
 
     only = set(filter(None, args.only.split(",")))

@@ -308,6 +308,7 @@ struct Overrides {
   int moe_decode = 1;
   int moe_depth = 3;
   int moe_wpb = 1;
+  int moe_nt = -1;
   bool any = false;  // some override is set (plans are then checked for an instance)
 };
 
@@ -343,6 +344,7 @@ const Overrides& overrides() {
     env_int("MARLIN_MI355X_MOE_DECODE", r.moe_decode);
     env_int("MARLIN_MI355X_MOE_DEPTH", r.moe_depth);
     env_int("MARLIN_MI355X_MOE_WPB", r.moe_wpb);
+    env_int("MARLIN_MI355X_MOE_NT", r.moe_nt);
     return r;
   }();
   return o;
@@ -379,8 +381,11 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // split K; N = 14336, 224 groups, stays at 64 columns: 9.5 against 11.9 us)
     if (int_operand && N / 64 <= cus / 2) nt = 2, depth = 4, occ = 1;
     // with no more 16-column groups than CUs, 16-column groups keep every CU streaming
-    // (cfg1 4096x4096: 6.1 us against 6.8 us with 32-column groups on half the CUs)
-    if (int_operand && N % 16 == 0 && N / 16 <= cus) nt = 1, depth = 4, occ = 1;
+    // (cfg1 4096x4096: 6.1 us against 6.8 us with 32-column groups on half the CUs), each
+    // by a 16-wave workgroup that splits K into two steps per wave, all in flight at once
+    // (cfg1 M = 16 / 1: 5.75 / 4.97 us against 6.27 / 5.91 us with four waves of eight
+    // steps; the same form on fp4 weights or wider N was slower, so it stays here)
+    if (int_operand && N % 16 == 0 && N / 16 <= cus) nt = 1, depth = 3, wpb = 16, occ = 1;
     // MXFP4 from four rows on: 64-column groups (cfg4 shape, M = 4 / 8 / 16: 9.1 / 9.0 / 9.6
     // against 9.9 / 10.0 / 10.4 us with 32-column groups; NVFP4 keeps 32 columns at every M)
     if (kinds.fmt == FMT_MXFP4 && M >= 4) nt = 4;
@@ -1119,7 +1124,8 @@ static marlin_status_t moe_gemm(bool gated,
     const int bm = moe_block_size <= 16 ? 16 : (int)moe_block_size;  // 8 -> 16 rows
     // column blocks of the multistage kernel: 4 waves x nt n16 tiles; the widest that divides
     // size_n (the reference requires size_n % 64, ops.cu:390-392)
-    const int nt = size_n % 256 == 0 ? 4 : (size_n % 128 == 0 ? 2 : 1);
+    int nt = size_n % 256 == 0 ? 4 : (size_n % 128 == 0 ? 2 : 1);
+    if (ov.moe_nt > 0 && size_n % (64 * ov.moe_nt) == 0) nt = ov.moe_nt;
     const int m_blocks = (int)((sorted_numel + moe_block_size - 1) / moe_block_size);
     const int n_blocks = (int)(size_n / (64 * nt));
     const int steps = (int)(size_k / 128);

@@ -48,7 +48,8 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     MMI_DECODE(4, 3, 1, true, true, 1)
     MMI_DECODE(4, 4, 1, true, true, 1)
     if constexpr (FMT != FMT_MXFP4 && FMT != FMT_NVFP4 && GSM != GSM_SMALL) {
-      MMI_DECODE(1, 4, 4, true, false, 1)  // 16-column groups: small N at M <= 16
+      // 16-column groups for small N at M <= 16: 16 waves split K, every step in flight
+      MMI_DECODE(1, 3, 16, true, false, 1)
     }
 #undef MMI_DECODE
     return hipErrorInvalidValue;
