@@ -38,7 +38,8 @@ def test_moe_align_kat():
 
 @pytest.mark.parametrize("tokens,E,topk,bs", [(16, 256, 8, 64), (2048, 256, 8, 64), (7, 8, 2, 16),
                                                (300, 64, 6, 8), (1000, 128, 4, 48),
-                                               (3000, 512, 8, 32), (5000, 1024, 8, 16)])
+                                               (3000, 512, 8, 32), (5000, 1024, 8, 16),
+                                               (8192, 256, 8, 64), (9000, 256, 8, 64)])
 @pytest.mark.parametrize("id_dtype", [torch.int32, torch.int64])
 def test_moe_align_matches_oracle(tokens, E, topk, bs, id_dtype):
     gen = torch.Generator().manual_seed(tokens + E)
@@ -242,6 +243,34 @@ def test_moe_gemm_multistage_integer(fmt, dtype, bs):
                                          tw.cuda(), bs, topk, mul, tid, T, N, H, b_zeros=zeros,
                                          global_scale=glob, is_zp_float=zeros is not None).cpu()
         assert O.max_abs_rel_err(out, _moe_ref(x, deq, ids, topk, tw, mul)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["u4", "u4b8", "u8b128"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,E,topk,bs,H", [
+    (600, 4, 2, 16, 256),    # 19 moe blocks per expert
+    (600, 4, 2, 64, 256),    # 5 moe blocks per expert
+    (2200, 2, 1, 16, 256),   # runs of more than 64 moe blocks of one expert
+    (160, 4, 2, 32, 1024),   # 8 K steps: split K
+    (96, 3, 2, 64, 288),     # a 32-deep K tail (channelwise uint8b128 only)
+])
+def test_moe_gemm_many_blocks_per_expert(fmt, dtype, T, E, topk, bs, H):
+    """The multistage MoE kernel with many consecutive moe blocks per expert, split K and a
+    K tail; every route (with its router weight) against the oracle."""
+    if fmt != "u8b128" and H % 128:
+        pytest.skip("128-deep groups need K % 128 == 0")
+    N = 256
+    print(f"case moe-blocks fmt={fmt} dtype={dtype} T={T} E={E} topk={topk} bs={bs} H={H}",
+          flush=True)
+    tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, H, N, dtype, 60)
+    gen = torch.Generator().manual_seed(T + bs + H)
+    x = torch.randn((T, H), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    out = capi.moe_wna16_marlin_gemm(x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(),
+                                     tw.cuda(), bs, topk, True, tid, T, N, H, b_zeros=zeros,
+                                     global_scale=glob, is_zp_float=zeros is not None).cpu()
+    assert O.max_abs_rel_err(out, _moe_ref(x, deq, ids, topk, tw, True)) <= TOL
 
 
 @pytest.mark.parametrize("fmt", ["u4", "u8b128", "mxfp4", "nvfp4"])
