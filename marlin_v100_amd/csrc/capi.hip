@@ -302,6 +302,7 @@ struct Overrides {
   int stream_max_m = 1 << 30;
   int small_group_max_m = 1024;
   int stream_nt = -1;
+  int stream_bm = -1;
   int xcd_group_m = -1;
   int moe_split_k = -1;
   int moe_group_m = 4;
@@ -338,6 +339,7 @@ const Overrides& overrides() {
     env_int("MARLIN_MI355X_STREAM_MAX_M", r.stream_max_m);
     env_int("MARLIN_MI355X_SMALL_GROUP_MAX_M", r.small_group_max_m);
     env_int("MARLIN_MI355X_STREAM_NT", r.stream_nt);
+    env_int("MARLIN_MI355X_STREAM_BM", r.stream_bm);
     env_int("MARLIN_MI355X_XCD_GROUP_M", r.xcd_group_m);
     env_int("MARLIN_MI355X_MOE_SPLIT_K", r.moe_split_k);
     env_int("MARLIN_MI355X_MOE_GROUP_M", r.moe_group_m);
@@ -479,16 +481,29 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= ov.small_group_max_m)
       bm = 32;
     int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
+    // 65..128 rows with at least one 256-column block per two CUs: one 128-row block (each
+    // weight dequantized once, 32x32 MFMAs) instead of two 64-row blocks (cfg2 N = 34816,
+    // M = 80 / 128: 79 / 82 against 90 / 93 us; N = 4096 / 8192 have too few blocks: 58 /
+    // 89 against 41 / 71 us at M = 128)
+    if (bm == 64 && M > 64 && nt == 4 && N / 256 >= cus / 2) bm = 128;
+    // fp4 weights beyond 384 rows: 64-row x 128-column blocks, so each weight is dequantized
+    // for twice the rows (cfg4 shape, M = 512 / 1024: MXFP4 61 / 115 against 76 / 137 us,
+    // NVFP4 65 / 125 against 92 / 164 us with 32 x 256 blocks; M <= 256 stays on 32 rows:
+    // 46 against 60 us)
+    const bool fp4_wide = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) && bm == 32 &&
+                          M > 384 && N % 128 == 0;
+    if (fp4_wide) bm = 64;
     // fp4 weights in 32-row blocks up to M = 64: 128-column tiles with at most two K splits
     // (cfg4 M=64: MXFP4 27.3 / NVFP4 28.6 us against 35.0 / 36.6 with 256-column tiles and
     // the occupancy-derived split; M = 512 keeps 256 columns; integer weights with small
     // groups are not measured here and keep the general rule)
     const bool small_group_narrow = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) &&
                                     bm == 32 && M <= 64 && N % 128 == 0;
-    if (small_group_narrow) nt = 2;
+    if (small_group_narrow || fp4_wide) nt = 2;
     if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
     if (ov.stream_nt >= 0) nt = ov.stream_nt;
-    const bool small_meta_fits = !(kinds.gsm == GSM_SMALL && bm >= 48);
+    if (ov.stream_bm > 0) bm = ov.stream_bm;
+    const bool small_meta_fits = !(kinds.gsm == GSM_SMALL && bm >= 48 && nt >= 4);
     if (nt > 0 && N % (64 * nt) == 0 && small_meta_fits) {
       p.bm = bm;
       p.nt = nt;

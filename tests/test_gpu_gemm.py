@@ -131,6 +131,10 @@ BASELINE_SHAPES = [
     ("cfg4", "nvfp4", torch.bfloat16, 1, 3072, 12288),
     ("cfg4", "nvfp4", torch.bfloat16, 64, 3072, 12288),
     ("cfg4", "nvfp4", torch.bfloat16, 512, 3072, 12288),
+    # a partial 128-row block (65..128 rows on wide N) and ragged 64-row fp4 blocks
+    ("cfg2", "u4", torch.bfloat16, 80, 5120, 34816),
+    ("cfg4", "nvfp4", torch.bfloat16, 1000, 3072, 12288),
+    ("cfg4", "mxfp4", torch.bfloat16, 777, 3072, 12288),
 ]
 
 
