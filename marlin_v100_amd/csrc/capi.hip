@@ -486,20 +486,27 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // M = 80 / 128: 79 / 82 against 90 / 93 us; N = 4096 / 8192 have too few blocks: 58 /
     // 89 against 41 / 71 us at M = 128)
     if (bm == 64 && M > 64 && nt == 4 && N / 256 >= cus / 2) bm = 128;
-    // fp4 weights beyond 384 rows: 64-row x 128-column blocks, so each weight is dequantized
-    // for twice the rows (cfg4 shape, M = 512 / 1024: MXFP4 61 / 115 against 76 / 137 us,
-    // NVFP4 65 / 125 against 92 / 164 us with 32 x 256 blocks; M <= 256 stays on 32 rows:
-    // 46 against 60 us)
+    // fp4 weights beyond 320 rows: 64-row x 128-column blocks, so each weight is dequantized
+    // for twice the rows (cfg4 shape, M = 384 / 512 / 1024: MXFP4 57 / 61 / 115 against 76 /
+    // 76 / 137 us, NVFP4 M = 512 / 1024: 65 / 125 against 92 / 164 us with 32 x 256 blocks;
+    // M = 192 / 256 stay on 32 rows: 46 / 45 against 53 / 62 us)
     const bool fp4_wide = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) && bm == 32 &&
-                          M > 384 && N % 128 == 0;
+                          M > 320 && N % 128 == 0;
     if (fp4_wide) bm = 64;
-    // fp4 weights in 32-row blocks up to M = 64: 128-column tiles with at most two K splits
-    // (cfg4 M=64: MXFP4 27.3 / NVFP4 28.6 us against 35.0 / 36.6 with 256-column tiles and
-    // the occupancy-derived split; M = 512 keeps 256 columns; integer weights with small
-    // groups are not measured here and keep the general rule)
+    // fp4 weights at 17..128 rows: 16-row blocks, 128 columns wide once that gives about 1.5
+    // blocks per CU, else 64, with at most two K splits (cfg4 shape, MXFP4 M = 32 / 64 / 128:
+    // 17.3 / 25.1 / 32.7 against 24.5 / 28.0 / 44.5 us with 32-row blocks; NVFP4 M = 64 /
+    // 128: 28.3 / 40.5 against 29.5 / 51.3 us; MXFP4 M = 64, K = N = 4096: 16.4 against 26.1
+    // us).  More rows per block would dequantize each weight fewer times, but at these sizes
+    // the grid's width, not the dequantization, sets the time.  (Integer weights with small
+    // groups are not measured here and keep the general rule.)
     const bool small_group_narrow = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) &&
-                                    bm == 32 && M <= 64 && N % 128 == 0;
-    if (small_group_narrow || fp4_wide) nt = 2;
+                                    M > 16 && M <= 128;
+    if (small_group_narrow) {
+      bm = 16;
+      nt = (N % 128 == 0 && ((M + 15) / 16) * (N / 128) * 2 >= 3 * (int64_t)cus) ? 2 : 1;
+    }
+    if (fp4_wide) nt = 2;
     if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
     if (ov.stream_nt >= 0) nt = ov.stream_nt;
     if (ov.stream_bm > 0) bm = ov.stream_bm;
@@ -511,7 +518,8 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       p.stream = 1;
       p.m_blocks = (int)((M + bm - 1) / bm);
       p.n_blocks = (int)(N / (64 * nt));
-      p.xcd_group_m = ov.xcd_group_m >= 0 ? ov.xcd_group_m : (bm >= 64 ? 4 : 0);
+      // (cfg3: groups of 8 block rows 588 against 605-615 us with 4; 16: 590-597 us)
+      p.xcd_group_m = ov.xcd_group_m >= 0 ? ov.xcd_group_m : (bm >= 64 ? 8 : 0);
       GemmLaunch q = kinds;
       q.bm = bm;
       q.nt = nt;
