@@ -366,7 +366,8 @@ const Overrides& overrides() {
 //  * Larger M is MFMA bound: 64x256 or 128x256 blocks (each wave 64/128 x 64) visited in the
 //    XCD-aware grouped order; split-K only when the grid cannot cover the CUs once.
 // MARLIN_MI355X_DECODE="nt,depth,wpb,ksplit,occ" (nt 0 disables the decode kernel),
-// MARLIN_MI355X_TILE="bm,nt,ch" and MARLIN_MI355X_SPLIT_K override the choice (tuning).
+// MARLIN_MI355X_TILE="bm,nt,ch" (tiled kernel), MARLIN_MI355X_STREAM_BM / _STREAM_NT
+// (multistage kernel) and MARLIN_MI355X_SPLIT_K override the choice (tuning).
 Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& kinds) {
   const Overrides& ov = overrides();
   Plan p{};
