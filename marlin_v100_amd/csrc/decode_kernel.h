@@ -87,6 +87,7 @@ void marlin_decode_kernel(const GemmParams p) {
   int n_blk = KSPLIT ? blk : blk * WPB + wave;
   int expert = 0;
   int route = -1;      // MoE: route index of block row `lane`
+  float route_w = 1.0f;  // MoE: its router weight (1 without mul_topk), read once here
   uint64_t live = 1;   // MoE: rows holding routes
   int nparts = 1;
   if constexpr (MOE) {
@@ -101,6 +102,7 @@ void marlin_decode_kernel(const GemmParams p) {
       const int id = p.sorted_ids[si];
       if (id >= 0 && id < p.valid_ids) route = id;
     }
+    if (p.mul_topk && route >= 0) route_w = p.topk_w[route];
     live = __ballot(route >= 0);
     nparts = (p.moe_bs + 15) >> 4;
   }
@@ -460,7 +462,7 @@ void marlin_decode_kernel(const GemmParams p) {
   if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[expert], p.alpha_exp);
   const uint16_t* bias = reinterpret_cast<const uint16_t*>(p.bias);
   uint16_t* cout = reinterpret_cast<uint16_t*>(p.c);
-  auto finish = [&](int row, int col, float v) __attribute__((always_inline)) {
+  auto finish = [&](int row, int col, float v, float w) __attribute__((always_inline)) {
     float o = v * alpha;
     if (bias != nullptr) {
       float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
@@ -471,7 +473,7 @@ void marlin_decode_kernel(const GemmParams p) {
       o += bv;
     }
     if constexpr (MOE) {
-      if (p.mul_topk) o *= p.topk_w[row];
+      if (p.mul_topk) o *= w;
     }
     cout[(int64_t)row * p.N + col] = to_raw16(o, AT{});
   };
@@ -481,9 +483,10 @@ void marlin_decode_kernel(const GemmParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int id = __shfl(row_id, lg * 4 + e);
+      const float w = __shfl(route_w, part * 16 + lg * 4 + e);
       if (id >= 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) finish(id, (tn0 + t) * 16 + ln, acc[t][e]);
+        for (int t = 0; t < NT; ++t) finish(id, (tn0 + t) * 16 + ln, acc[t][e], w);
       }
     }
     continue;
@@ -495,7 +498,7 @@ void marlin_decode_kernel(const GemmParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = lg * 4 + e;
-        if (row < p.M) finish(row, (tn0 + t) * 16 + ln, acc[t][e]);
+        if (row < p.M) finish(row, (tn0 + t) * 16 + ln, acc[t][e], 1.0f);
       }
     return;
   }
@@ -526,7 +529,7 @@ void marlin_decode_kernel(const GemmParams p) {
         const int col = (tn0 + t) * 16 + ln;
         const float v = __hip_atomic_exchange(p.ws + (int64_t)row * p.N + col, 0.0f,
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        finish(row, col, v);
+        finish(row, col, v, 1.0f);
       }
     }
   if (lane == 0)

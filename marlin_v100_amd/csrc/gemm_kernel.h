@@ -187,6 +187,7 @@ void marlin_gemm_kernel(const GemmParams p) {
   __shared__ u32x4_t lds_a0[FRAGS * 64];
   __shared__ u32x4_t lds_a1[FRAGS * 64];
   __shared__ int lds_rows[BM];
+  __shared__ float lds_w[BM];  // MoE: router weight of each block row (1 without mul_topk)
   __shared__ int lds_last;
 
   const int tid = threadIdx.x;
@@ -216,6 +217,8 @@ void marlin_gemm_kernel(const GemmParams p) {
         if (id < 0 || id >= p.valid_ids) id = -1;
       }
       lds_rows[r] = id;
+      // (read once here, not once per output element in the epilogue)
+      lds_w[r] = (p.mul_topk && id >= 0) ? p.topk_w[id] : 1.0f;
     }
     __syncthreads();
   }
@@ -444,7 +447,7 @@ void marlin_gemm_kernel(const GemmParams p) {
       o += bv;
     }
     if constexpr (MOE) {
-      if (p.mul_topk) o *= p.topk_w[orow];
+      if (p.mul_topk) o *= lds_w[r];
     }
     cout[orow * p.N + col] = to_raw16(o, AT{});
   };

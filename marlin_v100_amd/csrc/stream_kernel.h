@@ -64,6 +64,7 @@ void marlin_stream_kernel(const GemmParams p) {
   __shared__ u32x4_t lds_a1[FRAGS * 64];
   __shared__ u32x4_t lds_a2[FRAGS * 64];
   __shared__ int lds_rows[BM];
+  __shared__ float lds_w[BM];  // MoE: router weight of each block row (1 without mul_topk)
   __shared__ int lds_last;
   using Buf = u32x4_t[FRAGS * 64];
   auto buf = [&](auto dc) __attribute__((always_inline)) -> Buf& {
@@ -99,6 +100,8 @@ void marlin_stream_kernel(const GemmParams p) {
         if (id < 0 || id >= p.valid_ids) id = -1;
       }
       lds_rows[r] = id;
+      // (read once here, not once per output element in the epilogue)
+      lds_w[r] = (p.mul_topk && id >= 0) ? p.topk_w[id] : 1.0f;
     }
     __syncthreads();
   }
@@ -494,7 +497,7 @@ void marlin_stream_kernel(const GemmParams p) {
       o += bv;
     }
     if constexpr (MOE) {
-      if (p.mul_topk) o *= p.topk_w[orow];
+      if (p.mul_topk) o *= lds_w[r];
     }
     cout[orow * p.N + col] = to_raw16(o, AT{});
   };
@@ -522,7 +525,7 @@ void marlin_stream_kernel(const GemmParams p) {
 
   if constexpr (GATED) {
     // value of one output as the two-pass path stores it (finish() without the store)
-    auto stage1_value = [&](int64_t orow, int col, float v) __attribute__((always_inline)) {
+    auto stage1_value = [&](int r, int col, float v) __attribute__((always_inline)) {
       float o = v * alpha;
       if (bias != nullptr) {
         float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
@@ -530,7 +533,7 @@ void marlin_stream_kernel(const GemmParams p) {
         if (p.mul_topk) bv *= alpha;
         o += bv;
       }
-      if (p.mul_topk) o *= p.topk_w[orow];
+      if (p.mul_topk) o *= lds_w[r];
       return (uint32_t)to_raw16(o, AT{});
     };
     // Gate wave w and up wave w + 2 hold the two factors of the same outputs.  Each finishes
@@ -550,7 +553,7 @@ void marlin_stream_kernel(const GemmParams p) {
         // the gate wave hands over its second half, the up wave its first half
         if (up ? j < HALF : j >= HALF) {
           const int64_t orow = out_row(r);
-          mine[j * 64 + lane] = orow >= 0 ? (uint16_t)stage1_value(orow, col, v) : 0;
+          mine[j * 64 + lane] = orow >= 0 ? (uint16_t)stage1_value(r, col, v) : 0;
         }
         ++j;
       });
@@ -566,7 +569,7 @@ void marlin_stream_kernel(const GemmParams p) {
         const int64_t orow = out_row(r);
         if (orow < 0) return;
         const uint32_t other = mine[jj * 64 + lane];
-        const uint32_t self = stage1_value(orow, col, v);
+        const uint32_t self = stage1_value(r, col, v);
         const uint32_t g = up ? other : self;
         const uint32_t u = up ? self : other;
         cout[orow * half + (up ? col - half : col)] = to_raw16(silu_mul1<AT>(g, u), AT{});
