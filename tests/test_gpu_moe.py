@@ -253,13 +253,15 @@ def test_moe_gemm_multistage_integer(fmt, dtype, bs):
     (2200, 2, 1, 16, 256),   # runs of more than 64 moe blocks of one expert
     (160, 4, 2, 32, 1024),   # 8 K steps: split K
     (96, 3, 2, 64, 288),     # a 32-deep K tail (channelwise uint8b128 only)
+    (300, 4, 2, 64, 768),    # K % 384 == 0 with three 256-column blocks: the column walk
+    (300, 4, 2, 16, 1152),
 ])
 def test_moe_gemm_many_blocks_per_expert(fmt, dtype, T, E, topk, bs, H):
     """The multistage MoE kernel with many consecutive moe blocks per expert, split K and a
     K tail; every route (with its router weight) against the oracle."""
     if fmt != "u8b128" and H % 128:
         pytest.skip("128-deep groups need K % 128 == 0")
-    N = 256
+    N = 768 if H % 384 == 0 else 256
     print(f"case moe-blocks fmt={fmt} dtype={dtype} T={T} E={E} topk={topk} bs={bs} H={H}",
           flush=True)
     tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, H, N, dtype, 60)
