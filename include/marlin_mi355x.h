@@ -61,7 +61,13 @@ int marlin_abi_version(void);
  * Replaces torch.ops._C.gptq_marlin_repack
  * (reference csrc/quantization/marlin/gptq_marlin_repack.cu:399-469).
  * perm: optional act-order row permutation (perm_numel == size_k) or NULL/0.
- * is_a_8bit: the reference's legacy 8-bit-activation layout; rejected on this build.
+ * is_a_8bit: the reference's 8-bit-activation layout instead
+ * (gptq_marlin_repack.cu:225-335): 32 x 32 (k x n) tiles, k tiles outer; within a tile the
+ * words of thread th (0..31) and n8 slice s (0..3) are the B fragment of an m16n8k32 8-bit
+ * tensor-core MMA for column 16*(s/2) + 8*(s%2) + th/4, rows 4*(th%4) + {0..3} and the same
+ * rows + 16 (4-bit: word th*4 + s, nibble i = row 4*(th%4) + i/2 + 16*(i%2); 8-bit: words
+ * th*8 + 2*s + h, byte i = row 4*(th%4) + 16*h + i).  Not with perm (the reference rejects
+ * that combination).  The GEMM itself rejects 8-bit activations, as the reference's does.
  */
 marlin_status_t marlin_gptq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_weight_numel,
                                           const int32_t* perm, int64_t perm_numel,
@@ -74,11 +80,27 @@ marlin_status_t marlin_gptq_marlin_repack(const int32_t* b_q_weight, int64_t b_q
  * in AWQ interleave order) -> the same kernel layout as marlin_gptq_marlin_repack.
  * Replaces torch.ops._C.awq_marlin_repack
  * (reference csrc/quantization/marlin/awq_marlin_repack.cu:300-381).
+ * is_a_8bit: the 8-bit-activation layout of marlin_gptq_marlin_repack
+ * (awq_marlin_repack.cu:165-270).
  */
 marlin_status_t marlin_awq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_weight_numel,
                                          int64_t size_k, int64_t size_n, int64_t num_bits,
                                          int is_a_8bit, int32_t* out, int64_t out_numel,
                                          marlin_stream_t stream);
+
+/*
+ * W4A8-FP8 weight preprocess: every 4-bit code v of qweight becomes v - z when v >= z, else
+ * 15 - v, with z = 8 (qzeros NULL: GPTQ-style weights, any shape with numel * 8 % 256 == 0)
+ * or the code's AWQ zero point (qweight [size_k, size_n/8] int32, qzeros
+ * [size_k/group_size, size_n/8] int32: same word column and nibble, row k / group_size;
+ * size_k % 32 == 0, group_size % 8 == 0).  out may equal qweight (in place).
+ * Replaces torch.ops._C.marlin_int4_fp8_preprocess
+ * (reference csrc/quantization/marlin/marlin_int4_fp8_preprocess.cu:5-97).
+ */
+marlin_status_t marlin_int4_fp8_preprocess(const int32_t* qweight, int64_t qweight_rows,
+                                           int64_t qweight_cols, const int32_t* qzeros,
+                                           int64_t qzeros_rows, int64_t qzeros_cols, int32_t* out,
+                                           marlin_stream_t stream);
 
 /*
  * Dense mixed-precision GEMM: C[M,N] = A[M,K] . dequant(B)[K,N] (+ bias), fp32 accumulation.

@@ -46,6 +46,17 @@ def _awq_marlin_repack_fake(b_q_weight, size_k, size_n, num_bits, is_a_8bit=Fals
                        device=b_q_weight.device)
 
 
+def marlin_int4_fp8_preprocess(qweight: torch.Tensor, qzeros_or_none: torch.Tensor | None = None,
+                               inplace: bool = False) -> torch.Tensor:
+    """W4A8-FP8 code remap (reference marlin_int4_fp8_preprocess.cu:58-97)."""
+    return torch.ops._C.marlin_int4_fp8_preprocess(qweight, qzeros_or_none, inplace)
+
+
+@register_fake("_C::marlin_int4_fp8_preprocess")
+def _marlin_int4_fp8_preprocess_fake(qweight, qzeros_or_none=None, inplace=False):
+    return qweight if inplace else torch.empty_like(qweight)
+
+
 def gptq_marlin_moe_repack(b_q_weight: torch.Tensor, perm: torch.Tensor, size_k: int,
                            size_n: int, num_bits: int, is_a_8bit: bool = False) -> torch.Tensor:
     """Per-expert repack into [E, size_k/16, size_n*bits/2] (reference _custom_ops.py:1228-1248)."""

@@ -37,6 +37,7 @@ SIGNATURES = {
     "marlin_abi_version": (_I, []),
     "marlin_gptq_marlin_repack": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P]),
     "marlin_awq_marlin_repack": (_I, [_P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P]),
+    "marlin_int4_fp8_preprocess": (_I, [_P, _I64, _I64, _P, _I64, _I64, _P, _P]),
     "marlin_gemm": (_I, [_P, _I, _I64, _P, _P, _I64, _P, _I64, _P, _I, _I64, _I64, _I64, _P, _I64,
                          _P, _I, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I,
                          _I, _I, _I, _P]),
@@ -129,6 +130,19 @@ def awq_marlin_repack(b_q_weight, size_k, size_n, num_bits, is_a_8bit=False, out
     _check(load().marlin_awq_marlin_repack(_ptr(b_q_weight), b_q_weight.numel(), size_k, size_n,
                                            num_bits, int(is_a_8bit), _ptr(out), out.numel(),
                                            _stream()))
+    return out
+
+
+def marlin_int4_fp8_preprocess(qweight, qzeros=None, out=None):
+    """qzeros None: GPTQ-style codes (any shape); else AWQ [size_k, size_n/8] with zero points
+    [size_k/group_size, size_n/8].  out may be qweight (in place)."""
+    if out is None:
+        out = torch.empty_like(qweight)
+    rows = qweight.shape[0] if qweight.dim() else 1
+    cols = qweight.numel() // rows if rows else 0
+    zr, zc = (qzeros.shape[0], qzeros.shape[1]) if qzeros is not None else (0, 0)
+    _check(load().marlin_int4_fp8_preprocess(_ptr(qweight), rows, cols, _ptr(qzeros), zr, zc,
+                                             _ptr(out), _stream()))
     return out
 
 

@@ -903,8 +903,10 @@ marlin_status_t marlin_gptq_marlin_repack(const int32_t* b_q_weight, int64_t b_q
     check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_k_size = ", 16);
     check(size_n % 64 == 0, "size_n = ", size_n, " is not divisible by tile_n_size = ", 64);
     check(num_bits == 4 || num_bits == 8, "num_bits must be 4 or 8. Got = ", num_bits);
-    check_supported(!is_a_8bit,
-                    "is_a_8bit=true (8-bit activation layout) is not supported on this build");
+    // (the reference has no act-order form of the 8-bit-activation layout,
+    // gptq_marlin_repack.cu:250, 377-396)
+    check(!(is_a_8bit && perm_numel != 0), "Unsupported repack config: num_bits = ", num_bits,
+          ", has_perm = 1, is_a_8bit = 1");
     check(size_k % 32 == 0, "size_k = ", size_k,
           " is not divisible by 32 (the gfx950 layout packs 32-deep MFMA blocks)");
     const int64_t pack = 32 / num_bits;
@@ -916,6 +918,13 @@ marlin_status_t marlin_gptq_marlin_repack(const int32_t* b_q_weight, int64_t b_q
           " must be 0 or size_k = ", size_k);
     if (size_k == 0 || size_n == 0) return;
     check(b_q_weight != nullptr && out != nullptr, "null tensor pointer");
+    if (is_a_8bit) {
+      check_hip(launch_a8_repack(reinterpret_cast<const uint32_t*>(b_q_weight), false,
+                                 reinterpret_cast<uint32_t*>(out), size_k, size_n, (int)num_bits,
+                                 (hipStream_t)stream),
+                "gptq_marlin_repack launch");
+      return;
+    }
     check_hip(launch_gptq_repack(reinterpret_cast<const uint32_t*>(b_q_weight),
                                  perm_numel ? perm : nullptr, reinterpret_cast<uint32_t*>(out),
                                  size_k, size_n, (int)num_bits, (hipStream_t)stream),
@@ -931,8 +940,6 @@ marlin_status_t marlin_awq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_
     check(size_k % 16 == 0, "size_k = ", size_k, " is not divisible by tile_k_size = ", 16);
     check(size_n % 64 == 0, "size_n = ", size_n, " is not divisible by tile_n_size = ", 64);
     check(num_bits == 4 || num_bits == 8, "num_bits must be 4 or 8. Got = ", num_bits);
-    check_supported(!is_a_8bit,
-                    "is_a_8bit=true (8-bit activation layout) is not supported on this build");
     check(size_k % 32 == 0, "size_k = ", size_k,
           " is not divisible by 32 (the gfx950 layout packs 32-deep MFMA blocks)");
     const int64_t pack = 32 / num_bits;
@@ -942,10 +949,47 @@ marlin_status_t marlin_awq_marlin_repack(const int32_t* b_q_weight, int64_t b_q_
           size_k * size_n / pack);
     if (size_k == 0 || size_n == 0) return;
     check(b_q_weight != nullptr && out != nullptr, "null tensor pointer");
+    if (is_a_8bit) {
+      check_hip(launch_a8_repack(reinterpret_cast<const uint32_t*>(b_q_weight), true,
+                                 reinterpret_cast<uint32_t*>(out), size_k, size_n, (int)num_bits,
+                                 (hipStream_t)stream),
+                "awq_marlin_repack launch");
+      return;
+    }
     check_hip(launch_awq_repack(reinterpret_cast<const uint32_t*>(b_q_weight),
                                 reinterpret_cast<uint32_t*>(out), size_k, size_n, (int)num_bits,
                                 (hipStream_t)stream),
               "awq_marlin_repack launch");
+  });
+}
+
+marlin_status_t marlin_int4_fp8_preprocess(const int32_t* qweight, int64_t qweight_rows,
+                                           int64_t qweight_cols, const int32_t* qzeros,
+                                           int64_t qzeros_rows, int64_t qzeros_cols, int32_t* out,
+                                           marlin_stream_t stream) {
+  return guarded([&] {
+    const int64_t numel = qweight_rows * qweight_cols;
+    check(qweight_rows >= 0 && qweight_cols >= 0, "qweight shape must be non-negative");
+    int group_size = 1;
+    if (qzeros == nullptr) {
+      check(numel * 8 % 256 == 0, "qweight.numel() * 8 % 256 != 0");
+    } else {
+      // AWQ weights [size_k, size_n / 8] with zero points [size_k / group_size, size_n / 8]
+      check(qweight_rows % 32 == 0, "size_k % 32 != 0");
+      check(qzeros_rows > 0, "qzeros has no rows");
+      check(qweight_cols == qzeros_cols, "qweight.size(1) != qzeros.size(1)");
+      check(qweight_rows % qzeros_rows == 0, "qweight.size(0) % qzeros.size(0) != 0");
+      group_size = (int)(qweight_rows / qzeros_rows);
+      check(group_size % 8 == 0, "group_size % 8 != 0");
+    }
+    if (numel == 0) return;
+    check(qweight != nullptr && out != nullptr, "null tensor pointer");
+    check_hip(launch_int4_fp8_preprocess(reinterpret_cast<const uint32_t*>(qweight),
+                                         reinterpret_cast<uint32_t*>(out),
+                                         reinterpret_cast<const uint32_t*>(qzeros), numel,
+                                         qzeros ? qweight_cols : 1, group_size,
+                                         (hipStream_t)stream),
+              "marlin_int4_fp8_preprocess launch");
   });
 }
 

@@ -15,6 +15,11 @@ hipError_t launch_gptq_repack(const uint32_t* src, const int* perm, uint32_t* ou
                               int64_t size_n, int bits, hipStream_t stream);
 hipError_t launch_awq_repack(const uint32_t* src, uint32_t* out, int64_t size_k, int64_t size_n,
                              int bits, hipStream_t stream);
+hipError_t launch_a8_repack(const uint32_t* src, bool awq, uint32_t* out, int64_t size_k,
+                            int64_t size_n, int bits, hipStream_t stream);
+hipError_t launch_int4_fp8_preprocess(const uint32_t* q, uint32_t* out, const uint32_t* zeros,
+                                      int64_t words, int64_t row_words, int group_size,
+                                      hipStream_t stream);
 hipError_t launch_dequant(int fmt, const GemmParams& p, bool bf16, void* out, int gs_mode,
                           hipStream_t stream);
 hipError_t launch_moe_align(const void* topk, bool is64, int64_t numel, int E, int bs, int* sorted,

@@ -1,7 +1,7 @@
 // torch_ops.cpp -- thin TORCH_LIBRARY binding of the reference op schemas over the C ABI.
 //
 // Built twice: with MMI_EXT_NAME=_C it registers torch.ops._C.{marlin_gemm,
-// gptq_marlin_repack, awq_marlin_repack} (schemas byte-identical to the reference
+// gptq_marlin_repack, awq_marlin_repack, marlin_int4_fp8_preprocess} (schemas byte-identical to the reference
 // csrc/torch_bindings_marlin.cpp:6-21); with MMI_EXT_NAME=_moe_C it registers
 // torch.ops._moe_C.{topk_softmax, topk_sigmoid, grouped_topk, moe_align_block_size,
 // moe_wna16_marlin_gemm, moe_sum} (csrc/moe/torch_bindings_marlin.cpp:5-54).  The _C build also registers the inspection op
@@ -109,6 +109,35 @@ at::Tensor op_awq_marlin_repack(at::Tensor& b_q_weight, int64_t size_k, int64_t 
                                    size_n, num_bits, is_a_8bit, out.data_ptr<int32_t>(),
                                    out.numel(), cur_stream(b_q_weight)));
   return out;
+}
+
+// reference marlin_int4_fp8_preprocess.cu:58-97
+at::Tensor op_marlin_int4_fp8_preprocess(at::Tensor& qweight,
+                                         std::optional<at::Tensor> qzeros_or_none, bool inplace) {
+  TORCH_CHECK(qweight.device().is_cuda(), "qweight is not on GPU");
+  TORCH_CHECK(qweight.scalar_type() == at::ScalarType::Int, "qweight.dtype != torch.int32");
+  TORCH_CHECK(qweight.is_contiguous(), "qweight is not contiguous");
+  const at::OptionalDeviceGuard guard(qweight.device());
+  at::Tensor output = inplace ? qweight : torch::empty_like(qweight);
+  const int64_t rows = qweight.dim() >= 1 ? qweight.size(0) : 1;
+  const int64_t cols = rows ? qweight.numel() / rows : 0;
+  if (!qzeros_or_none.has_value()) {
+    rethrow(marlin_int4_fp8_preprocess(qweight.data_ptr<int32_t>(), rows, cols, nullptr, 0, 0,
+                                       output.data_ptr<int32_t>(), cur_stream(qweight)));
+    return output;
+  }
+  at::Tensor qzeros = *qzeros_or_none;
+  TORCH_CHECK(qweight.dim() == 2, "qweight must be [size_k, size_n / 8] with qzeros");
+  TORCH_CHECK(qzeros.device().is_cuda(), "qzeros is not on GPU");
+  TORCH_CHECK(qzeros.scalar_type() == at::ScalarType::Int, "qweight.dtype != torch.int32");
+  TORCH_CHECK(qzeros.device() == qweight.device(),
+              "qzeros is not on the same device with qweight");
+  TORCH_CHECK(qzeros.dim() == 2 && qzeros.is_contiguous(), "qzeros must be a contiguous 2-D tensor");
+  rethrow(marlin_int4_fp8_preprocess(qweight.data_ptr<int32_t>(), qweight.size(0),
+                                     qweight.size(1), qzeros.data_ptr<int32_t>(), qzeros.size(0),
+                                     qzeros.size(1), output.data_ptr<int32_t>(),
+                                     cur_stream(qweight)));
+  return output;
 }
 
 // reference marlin.cu:83-506
@@ -254,12 +283,16 @@ TORCH_LIBRARY(_C, ops) {
   ops.def(
       "awq_marlin_repack(Tensor b_q_weight, SymInt size_k, "
       "SymInt size_n, int num_bits, bool is_a_8bit) -> Tensor");
+  ops.def(
+      "marlin_int4_fp8_preprocess(Tensor qweight, "
+      "Tensor? qzeros_or_none, bool inplace) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(_C, CUDA, ops) {
   ops.impl("marlin_gemm", &op_marlin_gemm);
   ops.impl("gptq_marlin_repack", &op_gptq_marlin_repack);
   ops.impl("awq_marlin_repack", &op_awq_marlin_repack);
+  ops.impl("marlin_int4_fp8_preprocess", &op_marlin_int4_fp8_preprocess);
 }
 
 TORCH_LIBRARY(_marlin_mi355x, ops) {

@@ -108,6 +108,66 @@ def unpack_gptq(words: torch.Tensor, num_bits: int) -> torch.Tensor:
     return out.to(torch.int32)
 
 
+def a8_layout_index(size_k: int, size_n: int, num_bits: int):
+    """Source coordinates of every code slot of the reference's 8-bit-activation repack output
+    (is_a_8bit; gptq_marlin_repack.cu:225-335, awq_marlin_repack.cu:165-270): arrays
+    (k, n) of shape [words, pack], slot i of output word w holding code (k[w, i], n[w, i]).
+    32 x 32 (k x n) tiles, k tiles outer, 32*32/pack words each; word group (thread th,
+    n8 slice s) covers column 16*(s//2) + 8*(s%2) + th//4 and rows 4*(th%4) + {0..3} and the
+    same rows + 16 -- for 4-bit one word th*4 + s (pack_idx {0,4,1,5,2,6,3,7}: nibble i =
+    row + i//2 + 16*(i%2)), for 8-bit two words th*8 + 2*s + h (byte i = row + 16*h + i)."""
+    pack = 32 // num_bits
+    assert size_k % 32 == 0 and size_n % 32 == 0
+    tile_words = 32 * 32 // pack
+    words = size_k * size_n // pack
+    w = np.arange(words, dtype=np.int64)
+    tile, r = w // tile_words, w % tile_words
+    n_tiles = size_n // 32
+    kt, nt = tile // n_tiles, tile % n_tiles
+    if num_bits == 4:
+        th, s, h = r // 4, r % 4, np.zeros_like(r)
+    else:
+        th, s, h = r // 8, (r // 2) % 4, r % 2
+    n = nt * 32 + 16 * (s // 2) + 8 * (s % 2) + th // 4
+    k0 = kt * 32 + 4 * (th % 4)
+    i = np.arange(pack, dtype=np.int64)[None, :]
+    if num_bits == 4:
+        k = k0[:, None] + i // 2 + 16 * (i % 2)
+    else:
+        k = k0[:, None] + 16 * h[:, None] + i
+    return k, np.broadcast_to(n[:, None], k.shape)
+
+
+def a8_repack(q: np.ndarray, num_bits: int) -> np.ndarray:
+    """Logical codes q [K, N] -> the 8-bit-activation repack output as int32
+    [K/16, N*16/pack] (a8_layout_index)."""
+    size_k, size_n = q.shape
+    pack = 32 // num_bits
+    k, n = a8_layout_index(size_k, size_n, num_bits)
+    codes = q.astype(np.uint64)[k, n] & ((1 << num_bits) - 1)
+    shifts = (np.arange(pack, dtype=np.uint64) * num_bits)[None, :]
+    words = (codes << shifts).sum(axis=1).astype(np.uint32)
+    return words.view(np.int32).reshape(size_k // 16, size_n * 16 // pack)
+
+
+def int4_fp8_preprocess(words: np.ndarray, zeros: np.ndarray | None = None) -> np.ndarray:
+    """marlin_int4_fp8_preprocess.cu:8-56: every 4-bit code v becomes v - z if v >= z else
+    15 - v, with z = 8 (no zero points) or the code's AWQ zero point (same word column and
+    nibble, zero-point row k // group_size for weights [K, N/8], zero points [K/gs, N/8])."""
+    w = words.astype(np.int64) & 0xFFFFFFFF
+    if zeros is None:
+        z = np.full_like(w, 0x88888888)
+    else:
+        gs = words.shape[0] // zeros.shape[0]
+        z = np.repeat(zeros.astype(np.int64) & 0xFFFFFFFF, gs, axis=0)
+    out = np.zeros_like(w)
+    for i in range(8):
+        v = (w >> (4 * i)) & 15
+        zz = (z >> (4 * i)) & 15
+        out |= np.where(v >= zz, v - zz, 15 - v) << (4 * i)
+    return out.astype(np.uint32).view(np.int32).reshape(words.shape)
+
+
 # ---------------------------------------------------------------------------------------
 # e2m1 / e8m0 / e4m3 helpers
 # ---------------------------------------------------------------------------------------

@@ -117,9 +117,32 @@ def test_repack_rejections():
     assert "tile_k_size" in lib.marlin_get_last_error().decode()
     assert lib.marlin_gptq_marlin_repack(None, 0, None, 0, 128, 64, 3, 0, None, 0, None) == 1
     assert "num_bits must be 4 or 8" in lib.marlin_get_last_error().decode()
-    assert lib.marlin_gptq_marlin_repack(None, 0, None, 0, 128, 64, 4, 1, None, 0, None) == 2
+    # the 8-bit-activation layout has no act-order form (gptq_marlin_repack.cu:377-396)
+    assert lib.marlin_gptq_marlin_repack(None, 128 * 64 // 8, None, 128, 128, 64, 4, 1, None,
+                                         128 * 64 // 8, None) == 1
+    assert "Unsupported repack config" in lib.marlin_get_last_error().decode()
+    # ... but is otherwise accepted (empty sizes: validated, nothing launched)
+    assert lib.marlin_gptq_marlin_repack(None, 0, None, 0, 0, 64, 4, 1, None, 0, None) == 0
+    assert lib.marlin_awq_marlin_repack(None, 0, 0, 64, 8, 1, None, 0, None) == 0
     assert lib.marlin_awq_marlin_repack(None, 5, 128, 64, 4, 0, None, 0, None) == 1
     assert "Shape mismatch" in lib.marlin_get_last_error().decode()
+
+
+def test_int4_fp8_preprocess_rejections():
+    """marlin_int4_fp8_preprocess.cu:60-92."""
+    lib = capi.load()
+    fake = ctypes.c_void_p(16)  # never dereferenced: every case fails validation first
+    assert lib.marlin_int4_fp8_preprocess(fake, 3, 5, None, 0, 0, fake, None) == 1
+    assert "% 256 != 0" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_int4_fp8_preprocess(fake, 48, 4, fake, 3, 4, fake, None) == 1
+    assert "size_k % 32 != 0" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_int4_fp8_preprocess(fake, 64, 4, fake, 2, 8, fake, None) == 1
+    assert "qweight.size(1) != qzeros.size(1)" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_int4_fp8_preprocess(fake, 64, 4, fake, 3, 4, fake, None) == 1
+    assert "qweight.size(0) % qzeros.size(0) != 0" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_int4_fp8_preprocess(fake, 64, 4, fake, 16, 4, fake, None) == 1
+    assert "group_size % 8 != 0" in lib.marlin_get_last_error().decode()
+    assert lib.marlin_int4_fp8_preprocess(None, 0, 8, None, 0, 0, None, None) == 0
 
 
 def test_moe_rejections():

@@ -552,3 +552,98 @@ def test_quantize_g_idx_reconstruction_bound():
         deq = O.dequant_int_g_idx(q, s, fmt, torch.float32, g_idx, zp)
         err = (deq - w).abs()
         assert (err <= s[g_idx.long()] * 0.5 + 1e-6).all(), fmt
+
+
+# ---- 8-bit-activation repack layout and the W4A8 preprocess -------------------------------
+
+def _a8_reference_thread_walk(words: np.ndarray, size_k: int, size_n: int, bits: int):
+    """The reference kernel's own walk for is_a_8bit (gptq_marlin_repack.cu:14-17, 80-107,
+    224-334), restated loop by loop: a 32 x 32 tile's source words in shared-memory order,
+    then each of the 4 x 32 threads assembling its word(s)."""
+    pack = 32 // bits
+    mask = (1 << bits) - 1
+    tile_ints = 32 // pack
+    tile_size = 32 * 32 // pack
+    n_tiles = size_n // 32
+    src = words.astype(np.int64) & 0xFFFFFFFF
+    out = np.zeros(size_k * size_n // pack, dtype=np.int64)
+    for kt in range(size_k // 32):
+        for nt in range(n_tiles):
+            sh = src[kt * tile_ints:(kt + 1) * tile_ints, nt * 32:(nt + 1) * 32].ravel()
+            base = (kt * n_tiles + nt) * tile_size
+            for warp in range(4):
+                for th in range(32):
+                    tc_col, tc_row = th // 4, (th % 4) * 4
+                    cur_n = (warp // 2) * 16 + tc_col
+                    b1 = [int(sh[cur_n + 32 * i + (warp % 2) * 8]) for i in range(tile_ints)]
+                    vals = [0] * 8
+                    for i in range(4):
+                        ci, cp = (tc_row + i) // pack, (tc_row + i) % pack
+                        vals[i] = (b1[ci] >> (cp * bits)) & mask
+                        vals[4 + i] = (b1[ci + tile_ints // 2] >> (cp * bits)) & mask
+                    if bits == 4:
+                        order = [0, 4, 1, 5, 2, 6, 3, 7]
+                        out[base + th * 4 + warp] = sum(vals[order[i]] << (4 * i) for i in range(8))
+                    else:
+                        out[base + th * 8 + warp * 2] = sum(vals[i] << (8 * i) for i in range(4))
+                        out[base + th * 8 + warp * 2 + 1] = sum(vals[4 + i] << (8 * i) for i in range(4))
+    return out.astype(np.uint32).view(np.int32)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_a8_layout_matches_the_reference_thread_walk(bits):
+    rng = np.random.default_rng(bits)
+    k, n = 64, 96
+    q = rng.integers(0, 1 << bits, size=(k, n))
+    words = O.gptq_pack(torch.from_numpy(q), bits).numpy()
+    got = O.a8_repack(q, bits).ravel()
+    assert np.array_equal(got, _a8_reference_thread_walk(words, k, n, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_a8_layout_places_every_code_once(bits):
+    k, n = 64, 64
+    kk, nn = O.a8_layout_index(k, n, bits)
+    flat = (kk * n + nn).ravel()
+    assert np.array_equal(np.sort(flat), np.arange(k * n))
+
+
+def test_a8_8bit_words_are_mma_m16n8k32_b_fragments():
+    """8-bit: the two words of (thread th, n8 slice s) are the B fragment of an m16n8k32
+    s8 MMA (PTX ISA, mma.m16n8k32 .s8 fragment layout): column th // 4 of the slice, rows
+    (th % 4) * 4 + i (first word) and the same + 16 (second word)."""
+    kk, nn = O.a8_layout_index(32, 32, 8)
+    for th in range(32):
+        for s in range(4):
+            for h in range(2):
+                w = th * 8 + 2 * s + h
+                assert list(kk[w]) == [(th % 4) * 4 + 16 * h + i for i in range(4)]
+                assert set(nn[w]) == {16 * (s // 2) + 8 * (s % 2) + th // 4}
+
+
+def test_int4_fp8_preprocess_reference_kat():
+    """tests/test_marlin_dense.py:372-388 at a smaller size: nibbles packed two per int8,
+    viewed as int32; the result is v - 8 for v >= 8 and 15 - v otherwise, per nibble."""
+    gen = torch.Generator().manual_seed(7)
+    unpacked = torch.randint(0, 16, (128, 256), generator=gen, dtype=torch.int32)
+    packed = (unpacked[:, ::2] * 16 + unpacked[:, 1::2]).to(torch.int8).view(torch.int32)
+    got = O.int4_fp8_preprocess(packed.numpy())
+    want = torch.where(unpacked >= 8, unpacked - 8, 15 - unpacked)
+    want = (want[:, ::2] * 16 + want[:, 1::2]).to(torch.int8).view(torch.int32)
+    assert np.array_equal(got, want.numpy())
+
+
+def test_int4_fp8_preprocess_awq_brute_force():
+    rng = np.random.default_rng(3)
+    k, nw, gs = 64, 4, 32
+    q = rng.integers(0, 1 << 32, size=(k, nw), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    z = rng.integers(0, 1 << 32, size=(k // gs, nw), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    got = O.int4_fp8_preprocess(q, z).view(np.uint32)
+    for r in range(k):
+        for c in range(nw):
+            word = 0
+            for i in range(8):
+                v = (int(q.view(np.uint32)[r, c]) >> (4 * i)) & 15
+                zz = (int(z.view(np.uint32)[r // gs, c]) >> (4 * i)) & 15
+                word |= (v - zz if v >= zz else 15 - v) << (4 * i)
+            assert int(got[r, c]) == word
