@@ -260,6 +260,11 @@ void marlin_stream_kernel(const GemmParams p) {
             uint32_t x0, x1, y0, y1;
             b_words(bv, 2 * q, b, x0, x1);
             b_words(bv, 2 * q + 1, b, y0, y1);
+            // 8-bit words opaque here: left visible, the scheduler moves the lane swaps of a
+            // ring slot up to its loads, a trip early, and the wave waits for loads it has
+            // just issued (cfg3 shape: 592 -> 552 us; 4-bit words: 422 -> 436 us at cfg2
+            // M = 1024, so they stay visible)
+            if constexpr (BITS == 8) asm volatile("" : "+v"(x0), "+v"(y0), "+v"(x1), "+v"(y1));
             uint32_t w0[2], w1[2] = {0u, 0u};
             deal32(x0, y0, w0[0], w0[1]);
             if constexpr (BITS == 8) deal32(x1, y1, w1[0], w1[1]);
