@@ -208,13 +208,15 @@ void marlin_stream_kernel(const GemmParams p) {
   auto load = [&](int s, auto dc) __attribute__((always_inline)) { load_part(s, dc, -1); };
 
   // Write this wave's fragments of ring slot dc into LDS buffer dc.
-  auto stage = [&](auto dc) __attribute__((always_inline)) {
+  // (part q: the fragments whose index is q mod 4; part -1: all of them)
+  auto stage_part = [&](auto dc, int q) __attribute__((always_inline)) {
     constexpr int d = decltype(dc)::value;
     Buf& lb = buf(dc);
 #pragma unroll
     for (int i = 0; i < FPW; ++i)
-      lb[stage_unit(i)] = (INT_B && BITS == 4) ? a_perm_u4(ra[d][i]) : ra[d][i];
+      if (q < 0 || i % 4 == q) lb[stage_unit(i)] = (INT_B && BITS == 4) ? a_perm_u4(ra[d][i]) : ra[d][i];
   };
+  auto stage = [&](auto dc) __attribute__((always_inline)) { stage_part(dc, -1); };
 
   auto b_words = [&](const u32x4_t (&bv)[NT][NL], int t, int b, uint32_t& w0, uint32_t& w1) __attribute__((always_inline)) {
     if constexpr (BITS == 4) {
@@ -385,12 +387,18 @@ void marlin_stream_kernel(const GemmParams p) {
       // blocks' MFMAs (cfg2 M=128: 101 -> 94 us; MoE stage 1 at T=2048: 706 -> 667 us).  The
       // 128-row 32x32 form issues them up front (spread: 418 -> 436 us at M=1024).
       constexpr bool kSpread = !M32;
+      // 256-column blocks also stage the next step's fragments a quarter per k32 block, each
+      // right after the matching quarter of loads, so that fragment i waits for a load
+      // issued a whole trip before instead of the last quarter's (MoE stage 1 + 2 at
+      // T = 2048: 1080 -> 1051 us; 128-column blocks measured no better)
+      constexpr bool kSpreadStage = kSpread && NT >= 4;
       if constexpr (!kSpread) load(min(s + d + 2, last), std::integral_constant<int, (d + 2) % D>{});
-      stage(std::integral_constant<int, (d + 1) % D>{});
+      if constexpr (!kSpreadStage) stage(std::integral_constant<int, (d + 1) % D>{});
       compute_core(buf(dc), rb[d], rm[d], 4, [&](int q) __attribute__((always_inline)) {
         if constexpr (kSpread) {
           __builtin_amdgcn_sched_barrier(0);
           load_part(min(s + d + 2, last), std::integral_constant<int, (d + 2) % D>{}, q);
+          if constexpr (kSpreadStage) stage_part(std::integral_constant<int, (d + 1) % D>{}, q);
           __builtin_amdgcn_sched_barrier(0);
         }
       });
