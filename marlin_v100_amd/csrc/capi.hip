@@ -530,7 +530,13 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
       const int64_t base = (int64_t)p.m_blocks * p.n_blocks;
       const int steps = (int)(K / 128);
       int splits = 1;
-      if (base < resident && steps >= 8)
+      // Split K only while the partial sums stay few: each split adds M x N device-scope
+      // atomics, which cost more than the idle CUs they fill from about half a million
+      // outputs on (split 1 against the split choice: cfg4 MXFP4 M = 64 20.0 / 22.2 us, uint4
+      // M = 128 N = 32768 85 / 111 us, uint8b128 M = 256 K = N = 4096 61 / 86 us; below the
+      // limit splitting still wins: uint4 M = 64 K = N = 4096 40 / 43 us, M = 48 K = 8192
+      // N = 2048 30 / 80 us, MXFP4 M = 64 K = N = 4096 14.0 / 16.3 us)
+      if (base < resident && steps >= 8 && M * N <= (int64_t(1) << 19))
         splits = (int)std::min<int64_t>(resident / base, steps / 4);
       if (small_group_narrow) splits = std::min(splits, 2);
       if (ov.split_k >= 0) splits = ov.split_k;

@@ -52,15 +52,17 @@ def test_no_alloc_large_m_then_repeat():
 
 
 def test_no_alloc_rejects_scratch_beyond_limit():
-    # M = 1024, N = 4096, K = 1024: 8 x 16 blocks of 128 x 256 on 256 CUs split K in two and
-    # need 4M partial sums, above the 2M the static scratch holds
-    case = make_case("u4b8", 1024, 4096, torch.float16, seed=3)
+    # M = 1280, N = 2048, K = 1024, uint4b8 in 32-deep groups: beyond 1024 rows small groups
+    # take the tiled kernel, whose 10 x 8 blocks of 128 x 256 on 256 CUs split K in two and
+    # need M * N = 2.6M partial sums, above the 2M the static scratch holds
+    m, k, n = 1280, 1024, 2048
+    case = make_case("u4b8", k, n, torch.float16, gs=32, seed=3)
     d = to_dev(case)
-    words = capi.gptq_marlin_repack(d.gptq_words, None, case.k, case.n, 4)
-    a = torch.randn((1024, 1024), generator=torch.Generator().manual_seed(4)).half().cuda()
+    words = capi.gptq_marlin_repack(d.gptq_words, None, k, n, 4)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(4)).half().cuda()
     with pytest.raises(capi.MarlinError, match="static scratch holds 2097152"):
-        capi.marlin_gemm_no_alloc(a, words, d.scales, case.type_id, 1024, 4096, 1024)
+        capi.marlin_gemm_no_alloc(a, words, d.scales, case.type_id, m, n, k)
     # the regular entry point runs the same shape
-    out = capi.marlin_gemm(a, words, d.scales, case.type_id, 1024, 4096, 1024)
-    rows = torch.arange(0, 1024, 37)
+    out = capi.marlin_gemm(a, words, d.scales, case.type_id, m, n, k)
+    rows = torch.arange(0, m, 37)
     assert O.max_abs_rel_err(out.cpu()[rows], O.gemm_ref(a.cpu()[rows], case.deq)) <= TOL
