@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of config keys to run")
+    ap.add_argument("--warm-seconds", type=float, default=None,
+                    help="wall time of untimed calls before each secondary workload (default "
+                         "0.1 s; counter runs pass 0, since every dispatch is profiled)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy (counter calibration for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
@@ -180,9 +183,13 @@ def meta_bytes(wt):
 WARM_SECONDS = 0.1
 
 
-def warm_up(fn_list, warmup, seconds=WARM_SECONDS):
-    """At least `warmup` calls, and calls until `seconds` of wall time have passed."""
+def warm_up(fn_list, warmup, seconds=None):
+    """At least `warmup` calls, and calls until `seconds` (default WARM_SECONDS) of wall time
+    have passed."""
     import torch
+
+    if seconds is None:
+        seconds = WARM_SECONDS
 
     n = len(fn_list)
     t0 = time.perf_counter()
@@ -195,7 +202,7 @@ def warm_up(fn_list, warmup, seconds=WARM_SECONDS):
     torch.cuda.synchronize()
 
 
-def time_calls(fn_list, steps, warmup, warm_seconds=WARM_SECONDS):
+def time_calls(fn_list, steps, warmup, warm_seconds=None):
     """Average per-call device time of rotating calls, HIP events on the current stream."""
     import torch
 
@@ -211,7 +218,7 @@ def time_calls(fn_list, steps, warmup, warm_seconds=WARM_SECONDS):
     return start.elapsed_time(end) / 1e3 / steps
 
 
-def time_queued(fn_list, steps, warmup, warm_seconds=WARM_SECONDS):
+def time_queued(fn_list, steps, warmup, warm_seconds=None):
     """Average per-call device time with the host out of the critical path: after an eager
     warm-up, a bounded spin kernel (torch.cuda._sleep) is queued ahead of the start event, so
     the GPU is busy while the host enqueues the K timed calls; they then run back to back and
@@ -240,7 +247,7 @@ SPIN_CYCLES = 50_000_000
 QUEUED_BELOW_US = 60.0
 
 
-def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed, warm_seconds=WARM_SECONDS):
+def dense_case(key, fmt, m, k, n, dtype, steps, warmup, seed, warm_seconds=None):
     import torch
 
     from marlin_v100_amd import ops
@@ -425,7 +432,10 @@ def cpu_baseline(m, k, n):
 
 
 def main() -> int:
+    global WARM_SECONDS
     args = parse()
+    if args.warm_seconds is not None:
+        WARM_SECONDS = args.warm_seconds
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is described in DESIGN.md, not run)"}))
