@@ -275,6 +275,48 @@ def test_moe_gemm_many_blocks_per_expert(fmt, dtype, T, E, topk, bs, H):
     assert O.max_abs_rel_err(out, _moe_ref(x, deq, ids, topk, tw, True)) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["u4", "u4b8", "u8b128"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,E,topk,bs,K,N,skew", [
+    (5, 8, 2, 16, 384, 256, False),     # three K steps
+    (12, 4, 3, 64, 768, 320, False),    # five 64-column groups
+    (40, 8, 2, 64, 1152, 256, True),    # one expert takes ~40 routes: several 16-row parts
+    (3, 256, 8, 64, 384, 128, False),   # many experts, most blocks empty
+    (7, 8, 1, 8, 1536, 192, False),     # 8-row moe blocks
+    (30, 16, 4, 32, 3072, 128, True),
+])
+def test_moe_gemm_few_routes_parts_and_bias(fmt, dtype, T, E, topk, bs, K, N, skew):
+    """The few-routes MoE kernel (one wave per moe block x 64-column group) at K = 384 ..
+    3072, on blocks with several 16-row parts holding routes (skewed routing), many empty
+    experts and 8-row blocks: every route, with and without its router weight (and a bias),
+    against the oracle."""
+    print(f"case moe-few fmt={fmt} dtype={dtype} T={T} E={E} topk={topk} bs={bs} K={K} N={N}",
+          flush=True)
+    assert T * topk <= 16 * E  # the few-routes plan
+    tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, K, N, dtype, 70)
+    gen = torch.Generator().manual_seed(T + E + K)
+    x = torch.randn((T, K), generator=gen).to(dtype)
+    logits = torch.randn((T, E), generator=gen)
+    if skew:
+        logits[:, 0] += 6.0
+    tw, ids = O.route_topk(logits, topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    bias = (torch.randn((E, N), generator=gen) * 0.1).to(dtype)
+    flat = ids.reshape(-1)
+    for mul, with_bias in ((False, False), (True, True)):
+        out = capi.moe_wna16_marlin_gemm(
+            x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(), tw.cuda(), bs, topk, mul,
+            tid, T, N, K, b_zeros=zeros, global_scale=glob, is_zp_float=zeros is not None,
+            b_bias=O.marlin_permute_bias(bias).cuda() if with_bias else None).cpu()
+        ref = torch.empty((flat.numel(), N))
+        for r in range(flat.numel()):
+            v = x[r // topk].float() @ deq[flat[r]].float()
+            if with_bias:
+                v = v + bias[flat[r]].float()
+            ref[r] = v * tw.reshape(-1)[r] if mul else v
+        assert O.max_abs_rel_err(out, ref) <= TOL, (mul, with_bias)
+
+
 @pytest.mark.parametrize("fmt", ["u4", "u8b128", "mxfp4", "nvfp4"])
 @pytest.mark.parametrize("n", [320, 384])
 @pytest.mark.parametrize("T,bs", [(5, 16), (96, 16), (96, 48), (96, 64)])
