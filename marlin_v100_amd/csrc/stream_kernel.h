@@ -16,14 +16,20 @@
 //     before each LDS read.);
 //   * slots and buffers are compile-time indices (static_for), the loop body is
 //     branch-free, and prefetches past the last step are clamped to it, so the compiler's
-//     vmcnt bookkeeping is exact on every trip;
+//     vmcnt bookkeeping is exact on every trip; values that only a later step reads (fp4
+//     scale bytes, 8-bit words before their lane swaps) are kept opaque until that step, so
+//     the scheduler cannot pull their use up to the load;
+//   * the 16x16 form issues the next step's loads a quarter per k32 block, between the
+//     MFMAs; 256-column blocks also stage the following step's fragments a quarter at a
+//     time, each right after the loads of the same quarter;
+//   * split K (fp32 device-scope atomics) only up to 2^19 outputs (capi.hip);
 //   * integer and fp8 weights with >= 128-deep groups (at most two m-tiles: the per-group
 //     partial sums cost registers) or channelwise scales (any tile) use the integer-operand
 //     path (device_common.h): codes feed the MFMA, the scale / zero point is applied to the
 //     fp32 sums; the 4-bit activation permutation it needs is applied once, by the wave
 //     that stages the fragment;
-//   * split-K, the XCD-aware block order, the MoE row gather / scatter and the epilogue are
-//     those of marlin_gemm_kernel (gemm_kernel.h).
+//   * the split-K protocol, the XCD-aware block order, the MoE row gather / scatter and the
+//     epilogue are those of marlin_gemm_kernel (gemm_kernel.h).
 #pragma once
 
 #include "decode_kernel.h"
