@@ -494,18 +494,20 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     const bool fp4_wide = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) && bm == 32 &&
                           M > 320 && N % 128 == 0;
     if (fp4_wide) bm = 64;
-    // fp4 weights at 17..128 rows: 16-row blocks, 128 columns wide once that gives about 1.5
-    // blocks per CU, else 64, with at most two K splits (cfg4 shape, MXFP4 M = 32 / 64 / 128:
-    // 17.3 / 25.1 / 32.7 against 24.5 / 28.0 / 44.5 us with 32-row blocks; NVFP4 M = 64 /
-    // 128: 28.3 / 40.5 against 29.5 / 51.3 us; MXFP4 M = 64, K = N = 4096: 16.4 against 26.1
-    // us).  More rows per block would dequantize each weight fewer times, but at these sizes
-    // the grid's width, not the dequantization, sets the time.  (Integer weights with small
-    // groups are not measured here and keep the general rule.)
+    // fp4 weights at 17..128 rows: 16-row blocks, 64 columns wide while that gives at most
+    // three blocks per CU, else 128, with at most two K splits (cfg4 shape, MXFP4 M = 32 / 64
+    // / 128: 17.3 / 25.1 / 32.7 against 24.5 / 28.0 / 44.5 us with 32-row blocks; NVFP4 M =
+    // 64 / 128: 28.3 / 40.5 against 29.5 / 51.3 us; MXFP4 M = 64, K = N = 4096: 16.4 against
+    // 26.1 us.  64 against 128 columns, one K split: M = 64 MXFP4 / NVFP4 18.6 / 22.9 against
+    // 19.7 / 25.5 us; M = 96 / 128 MXFP4 31.7 / 37.4 against 26.8 / 27.4 us).  More rows per
+    // block would dequantize each weight fewer times, but at these sizes the grid's width,
+    // not the dequantization, sets the time.  (Integer weights with small groups are not
+    // measured here and keep the general rule.)
     const bool small_group_narrow = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) &&
                                     M > 16 && M <= 128;
     if (small_group_narrow) {
       bm = 16;
-      nt = (N % 128 == 0 && ((M + 15) / 16) * (N / 128) * 2 >= 3 * (int64_t)cus) ? 2 : 1;
+      nt = (N % 128 == 0 && ((M + 15) / 16) * (N / 64) > 3 * (int64_t)cus) ? 2 : 1;
     }
     if (fp4_wide) nt = 2;
     if ((bm > 16 && nt == 1) || (bm == 128 && nt != 4)) nt = 0;  // not instantiated: tiled kernel
