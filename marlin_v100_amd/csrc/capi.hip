@@ -487,12 +487,14 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
     // M = 80 / 128: 79 / 82 against 90 / 93 us; N = 4096 / 8192 have too few blocks: 58 /
     // 89 against 41 / 71 us at M = 128)
     if (bm == 64 && M > 64 && nt == 4 && N / 256 >= cus / 2) bm = 128;
-    // fp4 weights beyond 320 rows: 64-row x 128-column blocks, so each weight is dequantized
-    // for twice the rows (cfg4 shape, M = 384 / 512 / 1024: MXFP4 57 / 61 / 115 against 76 /
-    // 76 / 137 us, NVFP4 M = 512 / 1024: 65 / 125 against 92 / 164 us with 32 x 256 blocks;
-    // M = 192 / 256 stay on 32 rows: 46 / 45 against 53 / 62 us)
-    const bool fp4_wide = (kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4) && bm == 32 &&
-                          M > 320 && N % 128 == 0;
+    // NVFP4 weights beyond 128 rows: 64-row x 128-column blocks, so each weight (whose
+    // dequantization costs four times MXFP4's VALU) is dequantized for twice the rows (cfg4
+    // shape, M = 192 / 256 / 320 / 512: 42.2 / 42.7 / 44.2 / 63.7 against 49.7 / 51.3 / 53.1 /
+    // 67.1 us with 32 x 256 blocks).  MXFP4 stays on 32-row blocks: with its scale bytes kept
+    // opaque until use (device_common.h) 32 x 256 blocks are level or ahead (M = 384 / 512 /
+    // 768: 56.6 / 60.0 / 81.2 against 58.0 / 60.4 / 85.8 us with 64 x 128; M = 1024, K = N =
+    // 4096: 47.2 against 50.8 us).
+    const bool fp4_wide = kinds.fmt == FMT_NVFP4 && bm == 32 && M > 128 && N % 128 == 0;
     if (fp4_wide) bm = 64;
     // fp4 weights at 17..128 rows: 16-row blocks, 64 columns wide while that gives at most
     // three blocks per CU, else 128, with at most two K splits (cfg4 shape, MXFP4 M = 32 / 64
