@@ -300,7 +300,7 @@ struct Overrides {
   int split_k = -1;
   int stream = 1;
   int stream_max_m = 1 << 30;
-  int small_group_max_m = 1024;
+  int small_group_max_m = -1;  // -1: 2048 rows for fp4 weights, 1024 for integer small groups
   int stream_nt = -1;
   int stream_bm = -1;
   int xcd_group_m = -1;
@@ -477,9 +477,13 @@ Plan select_dense(int64_t M, int64_t N, int64_t K, int cus, const GemmLaunch& ki
   if (ov.stream != 0 && M <= ov.stream_max_m) {
     int bm = M <= 16 ? 16 : (M <= 32 ? 32 : (M <= 128 ? 64 : 128));
     // per-32/16 group metadata for 48+ rows does not fit the register budget: 32-row blocks
-    // up to M = 1024, the tiled kernel beyond (measured on cfg4 MXFP4: 35 / 75 / 252 us at
-    // M = 64 / 512 / 2048 against 47 / 184 / 211 us tiled)
-    if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= ov.small_group_max_m)
+    // up to M = 2048 for fp4 weights and 1024 for integer ones, the tiled kernel beyond
+    // (measured on cfg4 MXFP4: 35 / 75 at M = 64 / 512 against 47 / 184 us tiled; M = 1536 /
+    // 2048 / 4096: 154 / 204 / 417 against 201 / 203 / 400 us tiled)
+    const bool fp4_fmt = kinds.fmt == FMT_MXFP4 || kinds.fmt == FMT_NVFP4;
+    const int64_t small_group_max_m =
+        ov.small_group_max_m >= 0 ? ov.small_group_max_m : (fp4_fmt ? 2048 : 1024);
+    if (kinds.gsm == GSM_SMALL && bm >= 48 && M <= small_group_max_m)
       bm = 32;
     int nt = N % 256 == 0 ? 4 : (N % 128 == 0 ? 2 : 1);
     // 65..128 rows with at least one 256-column block per two CUs: one 128-row block (each

@@ -151,8 +151,8 @@ def test_gemm_baseline_shapes(name, fmt, dtype, m, k, n):
 
 # The tiled kernel (marlin_gemm_kernel) serves what the other two do not instantiate: M > 128
 # with N % 256 != 0 (16-row x 64-column tiles, split K when the grid is small) and groups
-# below 128 beyond M = 1024 (128 x 256 tiles).  K = 1056 leaves a 32-deep tail after the
-# 256-deep steps.
+# below 128 beyond M = 1024 (fp4 weights: beyond M = 2048; 128 x 256 tiles).  K = 1056 leaves
+# a 32-deep tail after the 256-deep steps.
 TILED_CASES = [(fmt, dt, m, n, k) for fmt in ("u4b8", "u4", "u8b128", "fp8")
                for dt in (torch.float16, torch.bfloat16)
                for m, n, k in ((129, 192, 1024), (200, 320, 1024))]
@@ -171,7 +171,7 @@ def test_gemm_tiled_kernel_narrow_n(fmt, dtype, m, n, k):
 @pytest.mark.parametrize("fmt,gs", [("u4", 32), ("u4b8", 64), ("mxfp4", None), ("nvfp4", None)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gemm_tiled_kernel_small_groups_large_m(fmt, gs, dtype):
-    m, k, n = 1100, 1024, 512
+    m, k, n = (2100 if fmt in ("mxfp4", "nvfp4") else 1100), 1024, 512
     print(f"case tiled-small-group fmt={fmt} gs={gs} dtype={dtype} m={m}", flush=True)
     case = make_case(fmt, k, n, dtype, gs=gs, seed=77)
     a = torch.randn((m, k), generator=torch.Generator().manual_seed(78)).to(dtype)
