@@ -234,9 +234,11 @@ marlin_status_t marlin_moe_wna16_marlin_gemm(
  * silu(h[:, :I]) * h[:, I:] as [size_m * top_k, size_n / 2] instead of h, rounded as
  * marlin_moe_wna16_marlin_gemm followed by marlin_silu_and_mul round it.  No counterpart op
  * in the reference: it fuses the reference's stage 1 and activation
- * (fused_marlin_moe.py:183-212, activation.py:45-52).  Only the multistage kernel's plans
- * are fused (larger batches, size_n % 256 == 0, no split K); for any other plan it returns
- * MARLIN_STATUS_NOT_SUPPORTED before launching anything, and the caller runs the two passes.
+ * (fused_marlin_moe.py:183-212, activation.py:45-52).  The multistage kernel's plans
+ * (size_n % 256 == 0, no split K) and the few-routes decode kernel's plans (integer or fp8
+ * weights with >= 128-deep groups or channelwise scales, at most 16 routes per expert on
+ * average) are fused; for any other plan it returns MARLIN_STATUS_NOT_SUPPORTED before
+ * launching anything, and the caller runs the two passes.
  */
 marlin_status_t marlin_moe_wna16_marlin_gemm_silu(
     const void* a, marlin_dtype_t a_dtype, void* c, const int32_t* b_q_weight,

@@ -1300,12 +1300,14 @@ static marlin_status_t moe_gemm(bool gated,
       l.grid = (unsigned)((int64_t)m_blocks * groups);
     }
     if (gated) {
-      // the fused activation runs in the multistage kernel's epilogue; any other plan (the
-      // few-routes decode kernel, a split K, narrower column blocks, the tiled kernel) is
-      // reported as NOT_SUPPORTED before anything launches, and the caller runs the two
-      // passes instead
-      check_supported(l.stream && l.depth == 0 && nt == 4 && splits == 1 && size_n % 256 == 0 &&
-                          !ov.any,
+      // the fused activation runs in the epilogue of the multistage kernel (256-column
+      // blocks, no split K) or of the few-routes decode kernel (one wave per block, its
+      // tiles 32 gate and the matching 32 up columns); any other plan (a split K, narrower
+      // column blocks, the tiled kernel) is reported as NOT_SUPPORTED before anything
+      // launches, and the caller runs the two passes instead
+      const bool stream_ok = l.stream && l.depth == 0 && nt == 4 && splits == 1 && size_n % 256 == 0;
+      const bool decode_ok = l.depth == 3 && l.wpb == 1 && size_n % 64 == 0;
+      check_supported((stream_ok || decode_ok) && !ov.any,
                       "the fused SiLU stage-1 epilogue does not cover this shape or batch");
       l.gated = true;
       check_supported(instantiated(l), "no gated moe kernel instance for this configuration");

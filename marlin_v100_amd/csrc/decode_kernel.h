@@ -27,7 +27,11 @@
 //     fp32 partial sums;
 //   * K split across workgroups (when the grid needs it): the split blocks come first in
 //     the grid, add fp32 partial sums into a workspace with device-scope atomics, and the
-//     last arriver of a column group finishes it (arrival counters, as in gemm_kernel.h).
+//     last arriver of a column group finishes it (arrival counters, as in gemm_kernel.h);
+//   * GATED (MoE stage 1 with the SiLU-gated activation fused, one wave per workgroup):
+//     a wave's four tiles are two gate tiles and the two up tiles N/2 columns later, so
+//     each lane holds both factors of its outputs and stores silu(gate) * up, rounded as
+//     stage 1's store followed by silu_and_mul would round it.
 #pragma once
 
 #include <type_traits>
@@ -48,10 +52,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 // OCC: waves per SIMD the register allocation must allow (1 = compiler's choice).  At
 // OCC >= 3 the activation slices, which hit in L2, are loaded one step later than the weights
 // (ALEAD < DEPTH - 1), so fewer ring slots are live at once.
-template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM, bool MOE, int OCC>
+template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM, bool MOE, int OCC,
+          bool GATED = false>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(OCC, 8)))
 void marlin_decode_kernel(const GemmParams p) {
   static_assert(!MOE || KSPLIT, "MoE blocks use the K-split workgroup layout");
+  static_assert(!GATED || (MOE && NT == 4 && WPB == 1), "gated: one-wave MoE blocks, 4 tiles");
   constexpr int BITS = fmt_bits(FMT);
   constexpr int NL = (BITS == 4) ? 1 : 2;  // 1 KiB chunks per tile per 128-deep step
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
@@ -106,7 +112,13 @@ void marlin_decode_kernel(const GemmParams p) {
     live = __ballot(route >= 0);
     nparts = (p.moe_bs + 15) >> 4;
   }
-  const int tn0 = n_blk * NT;
+  // n16 tile of the wave's tile t (GATED: tiles 0-1 are gate columns 32 n_blk.., tiles 2-3
+  // the up columns N/2 later)
+  const int tn0 = GATED ? 2 * n_blk : n_blk * NT;
+  const int up_skip = GATED ? (p.N >> 5) - 2 : 0;
+  auto col_tile = [&](int t) __attribute__((always_inline)) {
+    return tn0 + t + ((GATED && t >= 2) ? up_skip : 0);
+  };
 
   for (int part = 0; part < nparts; ++part) {
   // (every wave of the workgroup sees the same rows, so the part loop is uniform)
@@ -158,7 +170,7 @@ void marlin_decode_kernel(const GemmParams p) {
   if constexpr (GSM == GSM_CHANNEL && !INT_B) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
+      meta_ch[t] = make_meta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, col_tile(t) * 16 + ln));
   }
 
   u32x4_t ra[DEPTH][4];       // activations: 4 k32 blocks per step
@@ -169,14 +181,14 @@ void marlin_decode_kernel(const GemmParams p) {
     if constexpr (GSM == GSM_BIG) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        mv[t][0] = load_meta_raw<FMT, AT>(p, meta_base, k0 >> p.group_shift, (tn0 + t) * 16 + ln);
+        mv[t][0] = load_meta_raw<FMT, AT>(p, meta_base, k0 >> p.group_shift, col_tile(t) * 16 + ln);
     } else if constexpr (GSM == GSM_SMALL) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
           mv[t][b] = load_meta_raw<FMT, AT>(p, meta_base, (k0 + 32 * b + 8 * lg) >> p.group_shift,
-                                            (tn0 + t) * 16 + ln);
+                                            col_tile(t) * 16 + ln);
     }
   };
 
@@ -189,7 +201,7 @@ void marlin_decode_kernel(const GemmParams p) {
     issue_order();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const uint32_t* tp = bptr + t * 256 + (int64_t)s * NL * chunk_stride;
+      const uint32_t* tp = bptr + (col_tile(t) - tn0) * 256 + (int64_t)s * NL * chunk_stride;
 #pragma unroll
       for (int c = 0; c < NL; ++c)
         rb[d][t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(tp + c * chunk_stride));
@@ -395,7 +407,7 @@ void marlin_decode_kernel(const GemmParams p) {
                           : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int64_t n = (int64_t)(tn0 + t) * 16 + ln;
+      const int64_t n = (int64_t)col_tile(t) * 16 + ln;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         if (b < nblocks) {
@@ -425,7 +437,7 @@ void marlin_decode_kernel(const GemmParams p) {
   if constexpr (INT_B && GSM == GSM_CHANNEL) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, (tn0 + t) * 16 + ln));
+      const IMeta m = make_imeta<FMT, AT>(load_meta_raw<FMT, AT>(p, meta_base, 0, col_tile(t) * 16 + ln));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = m.S * acc[t][i];
@@ -478,6 +490,37 @@ void marlin_decode_kernel(const GemmParams p) {
     cout[(int64_t)row * p.N + col] = to_raw16(o, AT{});
   };
 
+  if constexpr (GATED) {
+    // both factors of an output are in this lane: round each as stage 1 would store it,
+    // then silu_and_mul's rounding (splits == 1)
+    auto stage1_value = [&](int col, float v, float w) __attribute__((always_inline)) {
+      float o = v * alpha;
+      if (bias != nullptr) {
+        float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
+                                  AT{});
+        if (p.mul_topk) bv *= alpha;
+        o += bv;
+      }
+      if (p.mul_topk) o *= w;
+      return (uint32_t)to_raw16(o, AT{});
+    };
+    const int half = p.N >> 1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int id = __shfl(row_id, lg * 4 + e);
+      const float w = __shfl(route_w, part * 16 + lg * 4 + e);
+      if (id >= 0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int col = col_tile(t) * 16 + ln;
+          const uint32_t g = stage1_value(col, acc[t][e], w);
+          const uint32_t u = stage1_value(col_tile(t + 2) * 16 + ln, acc[t + 2][e], w);
+          cout[(int64_t)id * half + col] = to_raw16(silu_mul1<AT>(g, u), AT{});
+        }
+      }
+    }
+    continue;
+  }
   if constexpr (MOE) {
     // accumulator row lg*4+e belongs to the route held by lane lg*4+e (splits == 1)
 #pragma unroll
@@ -486,7 +529,7 @@ void marlin_decode_kernel(const GemmParams p) {
       const float w = __shfl(route_w, part * 16 + lg * 4 + e);
       if (id >= 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) finish(id, (tn0 + t) * 16 + ln, acc[t][e], w);
+        for (int t = 0; t < NT; ++t) finish(id, col_tile(t) * 16 + ln, acc[t][e], w);
       }
     }
     continue;
@@ -498,7 +541,7 @@ void marlin_decode_kernel(const GemmParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = lg * 4 + e;
-        if (row < p.M) finish(row, (tn0 + t) * 16 + ln, acc[t][e], 1.0f);
+        if (row < p.M) finish(row, col_tile(t) * 16 + ln, acc[t][e], 1.0f);
       }
     return;
   }
@@ -509,7 +552,7 @@ void marlin_decode_kernel(const GemmParams p) {
     for (int e = 0; e < 4; ++e) {
       const int row = lg * 4 + e;
       if (row < p.M)
-        __hip_atomic_fetch_add(p.ws + (int64_t)row * p.N + (tn0 + t) * 16 + ln, acc[t][e],
+        __hip_atomic_fetch_add(p.ws + (int64_t)row * p.N + col_tile(t) * 16 + ln, acc[t][e],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   // Same ordering argument as the tiled kernel: completed memory-side atomics, then the
@@ -526,7 +569,7 @@ void marlin_decode_kernel(const GemmParams p) {
     for (int e = 0; e < 4; ++e) {
       const int row = lg * 4 + e;
       if (row < p.M) {
-        const int col = (tn0 + t) * 16 + ln;
+        const int col = col_tile(t) * 16 + ln;
         const float v = __hip_atomic_exchange(p.ws + (int64_t)row * p.N + col, 0.0f,
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         finish(row, col, v, 1.0f);

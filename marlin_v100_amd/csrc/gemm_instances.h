@@ -25,13 +25,20 @@ static hipError_t launch_or_query(const GemmLaunch& l, Kernel kernel, unsigned t
 
 template <int FMT, class AT, int GSM>
 static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream_t s) {
-  if (l.gated && (l.depth > 0 || !l.stream)) return hipErrorInvalidValue;  // multistage only
+  if (l.gated && !l.stream && l.depth == 0) return hipErrorInvalidValue;  // no tiled form
   if (l.depth > 0) {
 #define MMI_DECODE(NT_, D_, WPB_, KS_, MOE_, OCC_)                                           \
   if (l.nt == NT_ && l.depth == D_ && l.wpb == WPB_ && l.ksplit == KS_ && l.moe == MOE_ &&       \
-      l.occ == OCC_)                                                                         \
+      l.occ == OCC_ && !l.gated)                                                             \
     return launch_or_query(l, marlin_decode_kernel<FMT, AT, NT_, D_, WPB_, KS_, GSM, MOE_, OCC_>, \
                            64 * WPB_, p, s);
+    if constexpr (FMT != FMT_MXFP4 && FMT != FMT_NVFP4 && GSM != GSM_SMALL) {
+      // few-routes MoE stage 1 with the SiLU-gated activation fused (integer-operand formats,
+      // the ones the few-routes plan takes)
+      if (l.nt == 4 && l.depth == 3 && l.wpb == 1 && l.ksplit && l.moe && l.occ == 1 && l.gated)
+        return launch_or_query(
+            l, marlin_decode_kernel<FMT, AT, 4, 3, 1, true, GSM, true, 1, true>, 64, p, s);
+    }
     MMI_DECODE(4, 3, 4, true, false, 1)
     MMI_DECODE(4, 3, 4, true, false, 3)
     MMI_DECODE(4, 2, 4, true, false, 3)

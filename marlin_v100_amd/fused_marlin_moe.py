@@ -156,8 +156,10 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     extensions (not in the reference): `block_size_m` fixes the moe block size instead of the
     reference's heuristic; `fuse_activation` runs stage 1 with the SiLU-gated activation in
     its epilogue where the library's plan allows it (same bits as the two passes).  It is off
-    by default: on the BASELINE cfg5 shape the fused stage-1 kernel measured slower than stage
-    1 plus the activation pass (T = 2048: 661 against 608 + 29 us per kernel)."""
+    by default: on the BASELINE cfg5 shape the fused stage-1 kernels measured slower than
+    stage 1 plus the activation pass, at T = 2048 (661 against 608 + 29 us per kernel) and
+    for decode-sized batches (T = 16 / 32 / 64 layer: 160 / 248 / 347 against 157 / 238 /
+    338 us), where each wave streams two 2 KiB pieces N/2 apart instead of 4 KiB."""
     if inplace:
         assert output is None, "Conflicting request"
     if isinstance(activation, str):
@@ -211,7 +213,7 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
 
     default_silu = activation == MoEActivation.SILU and activation_func is apply_moe_activation
     fused = False
-    if fuse_activation and default_silu and m * topk > 16 * e and (2 * n) % 256 == 0:
+    if fuse_activation and default_silu:
         # stage 1 with silu(gate) * up in its epilogue: cache2 directly, no [T*topk, 2I]
         # intermediate and no activation pass (same bits as the two passes below)
         fused = _stage1_silu_fused(hidden_states, cache2, w1, bias1, w1_scale, global_scale1,

@@ -437,11 +437,42 @@ def test_moe_stage1_silu_fused_is_bit_exact(fmt, dtype, bs, bias, mul):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
-def test_moe_stage1_silu_fused_declines_decode_batches():
-    """Few routes per expert take the decode kernel, which the fused entry does not cover:
-    it reports NOT_SUPPORTED and launches nothing (fused_marlin_moe then runs two passes)."""
-    E, T, topk, K, I, bs = 16, 8, 2, 256, 256, 16
-    tid, words, scales, zeros, _g, _d = _make_experts("u4", E, K, 2 * I, torch.bfloat16, 5)
+@pytest.mark.parametrize("fmt", ["u4", "u4b8", "u8b128", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bias,mul", [(False, False), (True, True)])
+def test_moe_stage1_silu_fused_decode_batches_bit_exact(fmt, dtype, bias, mul):
+    """Few routes per expert take the decode kernel, whose fused form gives each wave two gate
+    and the two matching up tiles: same bits as stage 1 then silu_and_mul.  K = 640 is five
+    steps (one full trip of the three-deep ring and two after it); I = 192 is not a multiple
+    of 128 columns."""
+    E, T, topk, K, I, bs = 16, 8, 2, 640, 192, 16
+    print(f"case fused-silu-decode fmt={fmt} dtype={dtype} bias={bias} mul={mul}", flush=True)
+    tid, words, scales, zeros, glob, _d = _make_experts(fmt, E, K, 2 * I, dtype, 40)
+    gen = torch.Generator().manual_seed(41)
+    ids = torch.randint(0, E, (T, topk), generator=gen, dtype=torch.int32)
+    tw = torch.rand((T, topk), generator=gen)
+    s = torch.empty(ids.numel() + E * (bs - 1), dtype=torch.int32, device="cuda")
+    e = torch.empty(s.numel() // bs + 1, dtype=torch.int32, device="cuda")
+    npad = torch.empty(1, dtype=torch.int32, device="cuda")
+    capi.moe_align_block_size(ids.cuda(), E, bs, s, e, npad)
+    x = torch.randn((T, K), generator=gen).to(dtype).cuda()
+    b = (torch.randn((E, 2 * I), generator=gen) * 0.1).to(dtype).cuda() if bias else None
+    kw = dict(b_bias=b, global_scale=glob, b_zeros=zeros, is_zp_float=zeros is not None)
+    args = (x, words, scales, s, e, npad, tw.reshape(-1).cuda(), bs, topk, mul, tid, T, 2 * I, K)
+    h = capi.moe_wna16_marlin_gemm(*args, **kw)
+    ref = torch.empty((T * topk, I), dtype=dtype, device="cuda")
+    capi.silu_and_mul(ref, h)
+    out = torch.full((T * topk, I), float("nan"), dtype=dtype, device="cuda")
+    capi.moe_wna16_marlin_gemm(*args, c=out, silu_gated=True, **kw)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_moe_stage1_silu_fused_declines_tiled_plans():
+    """A plan with no fused form (fp4 small-group metadata in 64-row moe blocks takes the
+    tiled kernel) reports NOT_SUPPORTED and launches nothing (fused_marlin_moe then runs two
+    passes)."""
+    E, T, topk, K, I, bs = 4, 8, 2, 256, 256, 64
+    tid, words, scales, zeros, glob, _d = _make_experts("nvfp4", E, K, 2 * I, torch.bfloat16, 5)
     ids = torch.randint(0, E, (T, topk), dtype=torch.int32)
     s = torch.empty(ids.numel() + E * (bs - 1), dtype=torch.int32, device="cuda")
     e = torch.empty(s.numel() // bs + 1, dtype=torch.int32, device="cuda")
@@ -451,16 +482,16 @@ def test_moe_stage1_silu_fused_declines_decode_batches():
     out = torch.full((T * topk, I), 7.0, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(capi.MarlinError) as err:
         capi.moe_wna16_marlin_gemm(x, words, scales, s, e, npad, torch.ones(T * topk).cuda(), bs,
-                                   topk, False, tid, T, 2 * I, K, c=out, b_zeros=zeros,
-                                   is_zp_float=True, silu_gated=True)
+                                   topk, False, tid, T, 2 * I, K, c=out, global_scale=glob,
+                                   silu_gated=True)
     assert err.value.status == capi.STATUS_NOT_SUPPORTED
     torch.cuda.synchronize()
     assert (out == 7.0).all()
 
 
 def test_fused_marlin_moe_fuse_activation_matches_two_pass():
-    """fused_marlin_moe(fuse_activation=True) gives the two-pass layer's bits (batch large
-    enough for the multistage kernel)."""
+    """fused_marlin_moe(fuse_activation=True) gives the two-pass layer's bits, for a batch
+    large enough for the multistage kernel and for a decode-sized one."""
     from marlin_v100_amd.fused_marlin_moe import fused_marlin_moe
 
     T, E, topk, H, I = 200, 8, 2, 256, 128
@@ -475,3 +506,9 @@ def test_fused_marlin_moe_fuse_activation_matches_two_pass():
     one = fused_marlin_moe(x, w13, w2, None, None, s13, s2, tw.cuda(), ids.cuda(), tid,
                            fuse_activation=True, **kw)
     assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+    # a decode-sized batch (few-routes kernel's fused form): same bits as two passes
+    xs, tws, idss = x[:6].contiguous(), tw[:6].cuda(), ids[:6].cuda()
+    fused = fused_marlin_moe(xs, w13, w2, None, None, s13, s2, tws, idss, tid,
+                             fuse_activation=True, **kw)
+    unfused = fused_marlin_moe(xs, w13, w2, None, None, s13, s2, tws, idss, tid, **kw)
+    assert torch.equal(fused.view(torch.int16), unfused.view(torch.int16))
