@@ -1208,7 +1208,16 @@ static marlin_status_t moe_gemm(bool gated,
     // size_n (the reference requires size_n % 64, ops.cu:390-392)
     int nt = size_n % 256 == 0 ? 4 : (size_n % 128 == 0 ? 2 : 1);
     if (ov.moe_nt > 0 && size_n % (64 * ov.moe_nt) == 0) nt = ov.moe_nt;
-    const int m_blocks = (int)((sorted_numel + moe_block_size - 1) / moe_block_size);
+    // Moe blocks that can hold routes: every expert with routes has at least one route, so
+    // there are at most (routes + min(routes, E) (bs - 1)) / bs of them (expert ids index the
+    // num_experts weight slabs).  sorted_token_ids is sized for E (bs - 1) padding slots; with
+    // fewer routes than experts the blocks past this bound could only launch workgroups that
+    // read the padded total and exit (T = 16, E = 256, bs = 64: 128 instead of 254 blocks).
+    const int64_t routes = size_m * top_k;
+    const int64_t live_bound =
+        (routes + std::min<int64_t>(routes, num_experts) * (moe_block_size - 1)) / moe_block_size;
+    const int m_blocks = (int)std::min<int64_t>((sorted_numel + moe_block_size - 1) / moe_block_size,
+                                                live_bound);
     const int n_blocks = (int)(size_n / (64 * nt));
     const int steps = (int)(size_k / 128);
     // Only a fraction of the moe blocks are live; estimate them from the route count.
