@@ -96,6 +96,30 @@ def test_moe_gemm_stage1(fmt, dtype, bs):
     assert O.max_abs_rel_err(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("bs", [8, 16, 64])
+@pytest.mark.parametrize("fmt", ["u4", "mxfp4"])
+def test_moe_gemm_every_route_on_its_own_expert(bs, fmt):
+    """Fewer routes than experts, each route on a different expert: every route is a moe
+    block of its own, exactly as many blocks as the launch bound allows (routes + routes x
+    (bs - 1)) / bs, so a bound one block short would drop the last route."""
+    T, E, topk, H, N = 4, 64, 8, 256, 256
+    tid, words, scales, zeros, glob, deq = _make_experts(fmt, E, H, N, torch.bfloat16, 60)
+    gen = torch.Generator().manual_seed(61)
+    x = torch.randn((T, H), generator=gen).bfloat16()
+    ids = torch.randperm(E, generator=gen)[: T * topk].to(torch.int32).reshape(T, topk)
+    tw = torch.rand((T, topk), generator=gen)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    assert int(npad[0]) == T * topk * bs
+    out = capi.moe_wna16_marlin_gemm(x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(),
+                                     tw.reshape(-1).cuda(), bs, topk, False, tid, T, N, H,
+                                     b_zeros=zeros, global_scale=glob,
+                                     is_zp_float=zeros is not None).cpu()
+    ref = torch.empty((T * topk, N))
+    for r in range(T * topk):
+        ref[r] = x[r // topk].float() @ deq[ids.reshape(-1)[r]].float()
+    assert O.max_abs_rel_err(out, ref) <= TOL
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_moe_gemm_stage2_topk_weights_and_bias(dtype):
     T, E, topk, K, N, bs = 23, 8, 2, 256, 256, 16
