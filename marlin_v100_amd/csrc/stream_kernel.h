@@ -490,8 +490,13 @@ void marlin_stream_kernel(const GemmParams p) {
   }
 
   // ---- epilogue --------------------------------------------------------------------------
-  float alpha = 1.0f;
-  if constexpr (FMT == FMT_NVFP4) alpha = __builtin_ldexpf(p.global_scale[expert], p.alpha_exp);
+  // NVFP4: alpha scales the accumulator (global scale with the exponent-bias fold); a MoE
+  // bias under router weights is scaled by the global scale as passed, unfolded, as the
+  // reference's epilogue and bias init do (moe sm70_marlin_gemm.cuh:3490-3503,
+  // sm70_marlin_bias.cu:56-58)
+  float gscale = 1.0f;
+  if constexpr (FMT == FMT_NVFP4) gscale = p.global_scale[expert];
+  const float alpha = FMT == FMT_NVFP4 ? __builtin_ldexpf(gscale, p.alpha_exp) : 1.0f;
   const uint16_t* bias = reinterpret_cast<const uint16_t*>(p.bias);
   uint16_t* cout = reinterpret_cast<uint16_t*>(p.c);
 
@@ -511,7 +516,7 @@ void marlin_stream_kernel(const GemmParams p) {
       float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
                                 AT{});
       if constexpr (MOE) {
-        if (p.mul_topk) bv *= alpha;
+        if (p.mul_topk) bv *= gscale;
       }
       o += bv;
     }
@@ -549,7 +554,7 @@ void marlin_stream_kernel(const GemmParams p) {
       if (bias != nullptr) {
         float bv = raw16_to_float(load_u16<AT>(bias, (int64_t)expert * p.N + bias_storage_index(col)),
                                   AT{});
-        if (p.mul_topk) bv *= alpha;
+        if (p.mul_topk) bv *= gscale;
         o += bv;
       }
       if (p.mul_topk) o *= lds_w[r];

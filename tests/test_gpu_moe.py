@@ -96,6 +96,37 @@ def test_moe_gemm_stage1(fmt, dtype, bs):
     assert O.max_abs_rel_err(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("T", [6, 96])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_moe_gemm_nvfp4_bias_under_router_weights(T, dtype):
+    """NVFP4 with a bias and router weights: the bias is multiplied by the expert's global
+    scale as passed to the op, then by the router weight, as the reference's MoE epilogue and
+    bias init do (moe sm70_marlin_gemm.cuh:3490-3503, sm70_marlin_bias.cu:56-58); without
+    router weights it is added as is.  T = 6 / 96: few-routes and multistage moe blocks."""
+    E, topk, K, N, bs = 4, 2, 256, 256, 16
+    tid, words, scales, _z, glob, deq = _make_experts("nvfp4", E, K, N, dtype, 30)
+    gen = torch.Generator().manual_seed(31 + T)
+    x = torch.randn((T, K), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    # scaled so that the bias term stays comparable with the product under either rule
+    bias = (torch.randn((E, N), generator=gen) * 0.1 / glob.cpu().view(E, 1)).to(dtype)
+    flat = ids.reshape(-1)
+    for mul in (False, True):
+        out = capi.moe_wna16_marlin_gemm(
+            x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(), tw.cuda(), bs, topk, mul,
+            tid, T, N, K, global_scale=glob, b_bias=O.marlin_permute_bias(bias).cuda()).cpu()
+        ref = torch.empty((flat.numel(), N))
+        for r in range(flat.numel()):
+            ex = int(flat[r])
+            v = x[r // topk].float() @ deq[ex].float()
+            if mul:
+                ref[r] = (v + bias[ex].float() * float(glob[ex])) * tw.reshape(-1)[r]
+            else:
+                ref[r] = v + bias[ex].float()
+        assert O.max_abs_rel_err(out, ref) <= TOL, mul
+
+
 @pytest.mark.parametrize("bs", [8, 16, 64])
 @pytest.mark.parametrize("fmt", ["u4", "mxfp4"])
 def test_moe_gemm_every_route_on_its_own_expert(bs, fmt):

@@ -1,0 +1,74 @@
+"""Seeded random sweep of moe_wna16_marlin_gemm against the oracle, route by route: formats
+with >= 128-deep groups, channelwise scales and fp4, both dtypes, 2-16 experts, top-k 1-4,
+1-300 tokens (so both the few-routes decode kernel and the multistage / tiled moe blocks),
+every moe block size, K any multiple of 128 up to 1536, size_n any multiple of 64 up to 1024,
+with and without router weights and a bias.  Bar: max|out - ref| <= 1e-2 * max|ref|.
+As in the reference's MoE epilogue and bias init (moe sm70_marlin_gemm.cuh:3490-3503,
+sm70_marlin_bias.cu:56-58), an NVFP4 bias under router weights is multiplied by the global
+scale as passed to the op."""
+import math
+import random
+
+import pytest
+import torch
+
+import oracle as O
+from marlin_v100_amd import capi
+from tests.quant_cases import BITS, make_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+FMTS = ("u4b8", "u4", "u8b128", "u8", "fp8", "mxfp4", "nvfp4")
+
+
+def _case(i):
+    rng = random.Random(7000 + i)
+    fmt = FMTS[i % len(FMTS)]
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    e = rng.randint(2, 16)
+    topk = rng.randint(1, min(4, e))
+    t = max(1, int(round(2 ** rng.uniform(0, math.log2(300)))))
+    bs = rng.choice([8, 16, 32, 48, 64])
+    k = 128 * rng.randint(1, 12)
+    n = 64 * rng.randint(1, 16)
+    mul = rng.random() < 0.5
+    bias = rng.random() < 0.33
+    return fmt, dtype, e, topk, t, bs, k, n, mul, bias
+
+
+CASES = [_case(i) for i in range(35)]
+
+
+@pytest.mark.parametrize("i", range(len(CASES)))
+def test_moe_gemm_random_shapes(i):
+    fmt, dtype, E, topk, T, bs, K, N, mul, bias = CASES[i]
+    print(f"case moe-sweep {i}: fmt={fmt} dtype={dtype} E={E} topk={topk} T={T} bs={bs} K={K} "
+          f"N={N} mul={mul} bias={bias}", flush=True)
+    cases = [make_case(fmt, K, N, dtype, seed=800 + 31 * i + j) for j in range(E)]
+    words = torch.stack([capi.gptq_marlin_repack(c.gptq_words.cuda(), None, K, N, BITS[fmt])
+                         for c in cases])
+    scales = torch.stack([c.scales for c in cases]).cuda()
+    zeros = torch.stack([c.zeros for c in cases]).cuda() if cases[0].zeros is not None else None
+    glob = (torch.cat([c.global_scale for c in cases]).cuda()
+            if cases[0].global_scale is not None else None)
+    gen = torch.Generator().manual_seed(900 + i)
+    x = torch.randn((T, K), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    b = (torch.randn((E, N), generator=gen) * 0.1).to(dtype) if bias else None
+    out = capi.moe_wna16_marlin_gemm(
+        x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(), tw.cuda(), bs, topk, mul,
+        cases[0].type_id, T, N, K, b_zeros=zeros, global_scale=glob,
+        is_zp_float=zeros is not None,
+        b_bias=torch.stack([O.marlin_permute_bias(b[j]) for j in range(E)]).cuda()
+        if bias else None).cpu()
+    flat = ids.reshape(-1)
+    ref = torch.empty((flat.numel(), N))
+    for r in range(flat.numel()):
+        v = x[r // topk].float() @ cases[int(flat[r])].deq.float()
+        if bias:
+            g = float(glob[flat[r]]) if fmt == "nvfp4" and mul else 1.0
+            v = v + b[flat[r]].float() * g
+        ref[r] = v * tw.reshape(-1)[r] if mul else v
+    assert O.max_abs_rel_err(out, ref) <= TOL
