@@ -13,7 +13,9 @@ import torch
 
 import oracle as O
 from marlin_v100_amd import capi
-from tests.quant_cases import BITS, FORMATS, make_case, to_dev
+from marlin_v100_amd.marlin_utils import marlin_sort_g_idx
+from tests.quant_cases import BITS, FORMATS, TYPE_ID, make_case, to_dev
+from tests.test_gpu_act_order_zp import _act_order_case, _int_zp_case
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +37,7 @@ def _case(i):
     return fmt, dtype, gs, m, n, k, bias
 
 
-CASES = [_case(i) for i in range(56)]
+CASES = [_case(i) for i in range(112)]
 
 
 @pytest.mark.parametrize("i", range(len(CASES)))
@@ -54,3 +56,48 @@ def test_gemm_random_shapes(i):
                            global_scale=d.global_scale, b_zeros=d.zeros,
                            is_zp_float=d.zeros is not None).cpu()
     assert O.max_abs_rel_err(out, O.gemm_ref(a, case.deq, b)) <= TOL
+
+
+def _mode_case(i):
+    rng = random.Random(9500 + i)
+    mode = "act_order" if i % 2 else "int_zp"
+    fmt = rng.choice(("u4b8", "u4", "u8b128") if mode == "act_order" else ("u4", "u8"))
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    gs = rng.choice((-1, 64, 128) if mode == "act_order" else (-1, 32, 64, 128))
+    unit = max(gs, 32) if gs > 0 else 32
+    k = unit * rng.randint(2, 2048 // unit)
+    n = 64 * rng.randint(1, 24)
+    m = max(1, int(round(2 ** rng.uniform(0, math.log2(500)))))
+    return mode, fmt, dtype, gs, m, n, k
+
+
+MODE_CASES = [_mode_case(i) for i in range(40)]
+
+
+@pytest.mark.parametrize("i", range(len(MODE_CASES)))
+def test_gemm_random_shapes_int_zero_points_and_act_order(i):
+    """Random shapes for the two modes upstream marlin takes and the SM70 reference rejects:
+    packed integer zero points (the oracle's single rounding of (q - z) * s) and act-order
+    (weights repacked with perm = argsort(g_idx), every row scaled by its own group)."""
+    mode, fmt, dtype, gs, m, n, k = MODE_CASES[i]
+    print(f"case sweep-mode {i}: {mode} fmt={fmt} dtype={dtype} gs={gs} m={m} n={n} k={k}",
+          flush=True)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(700 + i)).to(dtype)
+    bits = BITS[fmt]
+    if mode == "int_zp":
+        q, s, z, _ = _int_zp_case(fmt, k, n, gs, dtype, seed=710 + i)
+        words = capi.gptq_marlin_repack(O.gptq_pack(q, bits).cuda(), None, k, n, bits)
+        out = capi.marlin_gemm(a.cuda(), words, s.cuda(), TYPE_ID[fmt], m, n, k,
+                               b_zeros=O.pack_cols(z, bits).cuda(), is_zp_float=False).cpu()
+        ref = O.gemm_ref(a, O.dequant_int_zero(q, s, z, dtype))
+    else:
+        g_idx, q, s, zp_f, deq = _act_order_case(fmt, k, n, gs, dtype, seed=720 + i)
+        g_sorted, perm = marlin_sort_g_idx(g_idx)
+        words = capi.gptq_marlin_repack(O.gptq_pack(q, bits).cuda(), perm.cuda(), k, n, bits)
+        out = capi.marlin_gemm(a.cuda(), words, s.cuda(), TYPE_ID[fmt], m, n, k,
+                               b_zeros=None if zp_f is None else zp_f.cuda(),
+                               is_zp_float=zp_f is not None, g_idx=g_sorted.cuda(),
+                               perm=perm.cuda()).cpu()
+        ref = O.gemm_ref(a, deq)
+    assert O.max_abs_rel_err(out, ref) <= TOL
+

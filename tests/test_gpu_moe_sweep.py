@@ -37,7 +37,7 @@ def _case(i):
     return fmt, dtype, e, topk, t, bs, k, n, mul, bias
 
 
-CASES = [_case(i) for i in range(35)]
+CASES = [_case(i) for i in range(70)]
 
 
 @pytest.mark.parametrize("i", range(len(CASES)))
