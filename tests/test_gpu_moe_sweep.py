@@ -9,6 +9,7 @@ scale as passed to the op."""
 import math
 import random
 
+import numpy as np
 import pytest
 import torch
 
@@ -72,3 +73,50 @@ def test_moe_gemm_random_shapes(i):
             v = v + b[flat[r]].float() * g
         ref[r] = v * tw.reshape(-1)[r] if mul else v
     assert O.max_abs_rel_err(out, ref) <= TOL
+
+
+def _align_case(i):
+    rng = random.Random(7500 + i)
+    e = max(1, int(round(2 ** rng.uniform(0, 10))))
+    topk = rng.randint(1, min(8, e))
+    t = max(1, int(round(2 ** rng.uniform(0, math.log2(12000)))))
+    bs = rng.choice([8, 16, 32, 48, 64])
+    id_dtype = rng.choice([torch.int32, torch.int64])
+    uniform = rng.random() < 0.3  # repeated and out-of-range ids instead of top-k routing
+    with_map = rng.random() < 0.3
+    if i % 10 == 9:  # more than 65536 routes: the multi-round one-workgroup kernel
+        e, topk, t = max(e, 8), 8, rng.randint(8200, 12000)
+    return e, topk, t, bs, id_dtype, uniform, with_map
+
+
+ALIGN_CASES = [_align_case(i) for i in range(40)]
+
+
+@pytest.mark.parametrize("i", range(len(ALIGN_CASES)))
+def test_moe_align_random_shapes(i):
+    """moe_align_block_size bit for bit against the oracle's stable order: 1-1024 experts,
+    up to ~96K routes (the one-workgroup, many-workgroup and multi-round paths), every block
+    size, int32 / int64 ids, ids outside [0, E) and expert maps with unmapped experts."""
+    E, topk, T, bs, id_dtype, uniform, with_map = ALIGN_CASES[i]
+    print(f"case align-sweep {i}: E={E} topk={topk} T={T} bs={bs} {id_dtype} uniform={uniform} "
+          f"map={with_map}", flush=True)
+    gen = torch.Generator().manual_seed(1200 + i)
+    if uniform:
+        ids = torch.randint(-1, E + 2, (T, topk), generator=gen)
+    else:
+        _, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    ids = ids.to(id_dtype)
+    emap = None
+    if with_map:
+        emap = torch.randint(-1, E, (E,), generator=gen, dtype=torch.int32)
+    numel = ids.numel()
+    s = torch.empty(numel + E * (bs - 1), dtype=torch.int32, device="cuda")
+    e = torch.empty(s.numel() // bs + 1, dtype=torch.int32, device="cuda")
+    n = torch.empty(1, dtype=torch.int32, device="cuda")
+    capi.moe_align_block_size(ids.cuda(), E, bs, s, e, n,
+                              None if emap is None else emap.cuda())
+    rs, re, rn = O.moe_align_block_size(ids.numpy(), E, bs,
+                                        expert_map=None if emap is None else emap.numpy())
+    assert int(n.cpu()[0]) == int(rn[0])
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(e.cpu().numpy(), re)
