@@ -120,3 +120,52 @@ def test_moe_align_random_shapes(i):
     assert int(n.cpu()[0]) == int(rn[0])
     assert np.array_equal(s.cpu().numpy(), rs)
     assert np.array_equal(e.cpu().numpy(), re)
+
+
+def _layer_case(i):
+    rng = random.Random(7800 + i)
+    fmt = ("u4", "u4b8", "u8b128", "mxfp4", "nvfp4")[i % 5]
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    e = rng.randint(2, 12)
+    topk = rng.randint(1, min(4, e))
+    t = max(1, int(round(2 ** rng.uniform(0, math.log2(400)))))
+    h = 128 * rng.randint(1, 4)
+    inter = 128 * rng.randint(1, 3)
+    return fmt, dtype, e, topk, t, h, inter
+
+
+LAYER_CASES = [_layer_case(i) for i in range(20)]
+
+
+@pytest.mark.parametrize("i", range(len(LAYER_CASES)))
+def test_fused_marlin_moe_random_layers(i):
+    """fused_marlin_moe (align, stage 1, SiLU-gated activation, stage 2 with router weights,
+    top-k sum; the block size from the reference's heuristic) against the oracle's per-token
+    layer at random sizes, within twice the GEMM tolerance (two GEMMs in a row)."""
+    from marlin_v100_amd.fused_marlin_moe import fused_marlin_moe
+
+    fmt, dtype, E, topk, T, H, I = LAYER_CASES[i]
+    print(f"case layer-sweep {i}: fmt={fmt} dtype={dtype} E={E} topk={topk} T={T} H={H} I={I}",
+          flush=True)
+
+    def experts(k, n, seed):
+        cases = [make_case(fmt, k, n, dtype, seed=seed + j) for j in range(E)]
+        words = torch.stack([capi.gptq_marlin_repack(c.gptq_words.cuda(), None, k, n, BITS[fmt])
+                             for c in cases])
+        scales = torch.stack([c.scales for c in cases]).cuda()
+        zeros = (torch.stack([c.zeros for c in cases]).cuda()
+                 if cases[0].zeros is not None else None)
+        glob = (torch.cat([c.global_scale for c in cases]).cuda()
+                if cases[0].global_scale is not None else None)
+        return cases[0].type_id, words, scales, zeros, glob, torch.stack([c.deq for c in cases])
+
+    tid, w13, s13, z13, g13, d13 = experts(H, 2 * I, 1000 + 37 * i)
+    _, w2, s2, z2, g2, d2 = experts(I, H, 2000 + 37 * i)
+    gen = torch.Generator().manual_seed(3000 + i)
+    x = torch.randn((T, H), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    out = fused_marlin_moe(x.cuda(), w13, w2, None, None, s13, s2, tw.cuda(), ids.cuda(), tid,
+                           global_scale1=g13, global_scale2=g2, w1_zeros=z13, w2_zeros=z2,
+                           is_w1_zp_float=z13 is not None, is_w2_zp_float=z2 is not None).cpu()
+    ref = O.moe_layer_ref(x, d13, d2, tw, ids)
+    assert O.max_abs_rel_err(out, ref) <= 2 * TOL

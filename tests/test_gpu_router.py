@@ -235,3 +235,36 @@ def test_grouped_topk_fallback_and_errors():
     with pytest.raises(RuntimeError, match="topk_group must be <= n_group"):
         ops.grouped_topk(torch.randn((2, 16), device="cuda"), 4, 5, 2, True, 1.0,
                          torch.zeros(16, device="cuda"), 0)
+
+
+def _router_case(i):
+    import math
+    import random
+
+    rng = random.Random(4000 + i)
+    e = max(1, int(round(2 ** rng.uniform(0, 12))))
+    k = rng.randint(1, min(e, 32))
+    t = max(1, int(round(2 ** rng.uniform(0, math.log2(3000)))))
+    dtype = rng.choice([torch.float32, torch.float16, torch.bfloat16])
+    scoring = rng.choice(["softmax", "sigmoid"])
+    renorm = rng.random() < 0.5
+    use_bias = rng.random() < 0.4
+    return t, e, k, dtype, scoring, renorm, use_bias
+
+
+ROUTER_CASES = [_router_case(i) for i in range(30)]
+
+
+@pytest.mark.parametrize("i", range(len(ROUTER_CASES)))
+def test_topk_random_shapes(i):
+    """Seeded random shapes (1-4096 experts, top-k up to 32, 1-3000 tokens, every gating dtype,
+    both scorings, with and without renormalization and a choice bias) against the oracle."""
+    T, E, k, dtype, scoring, renorm, use_bias = ROUTER_CASES[i]
+    print(f"case router-sweep {i}: T={T} E={E} k={k} {dtype} {scoring} renorm={renorm} "
+          f"bias={use_bias}", flush=True)
+    gen = torch.Generator().manual_seed(4100 + i)
+    gating = (torch.randn((T, E), generator=gen) * 2).to(dtype)
+    bias = (torch.randn(E, generator=gen) * 0.05) if use_bias else None
+    w, ids, tei = capi.topk_gating(gating.cuda(), k, renorm,
+                                   None if bias is None else bias.cuda(), scoring)
+    _check(gating, k, renorm, bias, scoring, w, ids, tei)
