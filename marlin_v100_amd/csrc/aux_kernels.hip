@@ -235,14 +235,23 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(
       rk[s] = r;
     }
     __syncthreads();
-    for (int x = tid; x < E; x += 1024) {
-      int run = 0;
-      for (int w = 0; w < 16; ++w) {
-        const int c = wave_cnt[w * E + x];
-        wave_cnt[w * E + x] = (uint16_t)run;
-        run += c;
+    if (numel - base <= 64 * kAlignPasses) {
+      // every route of the round is in wavefront 0 (the others' rows are zero): its counts
+      // are the round's, its exclusive prefix is zero
+      for (int x = tid; x < E; x += 1024) {
+        round_n[x] = wave_cnt[x];
+        wave_cnt[x] = 0;
       }
-      round_n[x] = run;
+    } else {
+      for (int x = tid; x < E; x += 1024) {
+        int run = 0;
+        for (int w = 0; w < 16; ++w) {
+          const int c = wave_cnt[w * E + x];
+          wave_cnt[w * E + x] = (uint16_t)run;
+          run += c;
+        }
+        round_n[x] = run;
+      }
     }
     __syncthreads();
   };

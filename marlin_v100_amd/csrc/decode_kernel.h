@@ -50,8 +50,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // OCC: waves per SIMD the register allocation must allow (1 = compiler's choice).  At
-// OCC >= 3 the activation slices, which hit in L2, are loaded one step later than the weights
-// (ALEAD < DEPTH - 1), so fewer ring slots are live at once.
+// OCC >= 2 the activation slices, which hit in L2, are loaded one step later than the weights
+// (ALEAD < DEPTH - 1), so fewer ring slots are live at once, and grouped integer-operand
+// tiles are multiplied and scaled two at a time.
 template <int FMT, class AT, int NT, int DEPTH, int WPB, bool KSPLIT, int GSM, bool MOE, int OCC,
           bool GATED = false>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(OCC, 8)))
@@ -62,7 +63,7 @@ void marlin_decode_kernel(const GemmParams p) {
   constexpr int NL = (BITS == 4) ? 1 : 2;  // 1 KiB chunks per tile per 128-deep step
   constexpr int RAWB = (GSM == GSM_SMALL) ? 4 : 1;
   static_assert(DEPTH >= 2 && DEPTH <= 4, "ring depth");
-  constexpr int ALEAD = (OCC >= 3 && DEPTH >= 3) ? DEPTH - 2 : DEPTH - 1;
+  constexpr int ALEAD = (OCC >= 2 && DEPTH >= 3) ? DEPTH - 2 : DEPTH - 1;
 
   const int lane = threadIdx.x & 63;
   // (readfirstlane: the wave index is uniform, so the K range, the loop counter and the
@@ -236,7 +237,7 @@ void marlin_decode_kernel(const GemmParams p) {
                           const MetaRaw (&mv)[NT][RAWB], int nblocks, auto permuted)
                           __attribute__((always_inline)) {
     constexpr bool PERMUTED = decltype(permuted)::value;
-    if constexpr (INT_B && GSM != GSM_CHANNEL && OCC >= 3) {
+    if constexpr (INT_B && GSM != GSM_CHANNEL && OCC >= 2) {
       // grouped, register-lean order: the step's row sums first, then the tiles two at a
       // time, each pair scaled into acc as soon as its four k32 blocks are multiplied
       f32x4_t r = f32x4_t{0.f, 0.f, 0.f, 0.f};

@@ -158,8 +158,8 @@ def fused_marlin_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
     its epilogue where the library's plan allows it (same bits as the two passes).  It is off
     by default: on the BASELINE cfg5 shape the fused stage-1 kernels measured slower than
     stage 1 plus the activation pass, at T = 2048 (661 against 608 + 29 us per kernel) and
-    for decode-sized batches (T = 16 / 32 / 64 layer: 160 / 248 / 347 against 157 / 238 /
-    338 us), where each wave streams two 2 KiB pieces N/2 apart instead of 4 KiB."""
+    for decode-sized batches (T = 16 / 32 / 64 layer: 161 / 246 / 342 against 142 / 214 /
+    299 us), where each wave streams two 2 KiB pieces N/2 apart instead of 4 KiB."""
     if inplace:
         assert output is None, "Conflicting request"
     if isinstance(activation, str):
