@@ -307,7 +307,7 @@ struct Overrides {
   int moe_split_k = -1;
   int moe_group_m = 4;
   int moe_decode = 1;
-  int moe_depth = 3;
+  int moe_depth = 2;
   int moe_wpb = 1;
   int moe_nt = -1;
   bool any = false;  // some override is set (plans are then checked for an instance)
@@ -1305,10 +1305,11 @@ static marlin_status_t moe_gemm(bool gated,
       // load-balances across CUs as they finish
       l.wpb = ov.moe_wpb;
       l.ksplit = true;
-      // two waves per SIMD (activations one step behind the weights, tiles scaled in
-      // pairs: no spills) rather than one wave with the compiler's full register choice:
-      // cfg5 layer at T = 16 / 64 / 300: 143 / 307 / 440 against 157 / 340 / 470 us
-      l.occ = (l.depth == 3 && l.wpb == 1) ? 2 : 1;
+      // two waves per SIMD (tiles scaled in pairs: no spills) rather than one wave with the
+      // compiler's full register choice, and a ring two steps deep: cfg5 layer at T = 16 /
+      // 64 / 300: 138 / 296 / 430 us, against 141 / 302 / 439 with three steps and 157 /
+      // 340 / 470 with one wave per SIMD
+      l.occ = (l.depth <= 3 && l.wpb == 1) ? 2 : 1;
       l.grid = (unsigned)((int64_t)m_blocks * groups);
     }
     if (gated) {
@@ -1318,7 +1319,7 @@ static marlin_status_t moe_gemm(bool gated,
       // column blocks, the tiled kernel) is reported as NOT_SUPPORTED before anything
       // launches, and the caller runs the two passes instead
       const bool stream_ok = l.stream && l.depth == 0 && nt == 4 && splits == 1 && size_n % 256 == 0;
-      const bool decode_ok = l.depth == 3 && l.wpb == 1 && size_n % 64 == 0;
+      const bool decode_ok = l.depth == 2 && l.wpb == 1 && size_n % 64 == 0;
       check_supported((stream_ok || decode_ok) && !ov.any,
                       "the fused SiLU stage-1 epilogue does not cover this shape or batch");
       l.gated = true;

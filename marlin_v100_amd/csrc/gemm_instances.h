@@ -35,9 +35,9 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     if constexpr (FMT != FMT_MXFP4 && FMT != FMT_NVFP4 && GSM != GSM_SMALL) {
       // few-routes MoE stage 1 with the SiLU-gated activation fused (integer-operand formats,
       // the ones the few-routes plan takes)
-      if (l.nt == 4 && l.depth == 3 && l.wpb == 1 && l.ksplit && l.moe && l.occ == 2 && l.gated)
+      if (l.nt == 4 && l.depth == 2 && l.wpb == 1 && l.ksplit && l.moe && l.occ == 2 && l.gated)
         return launch_or_query(
-            l, marlin_decode_kernel<FMT, AT, 4, 3, 1, true, GSM, true, 2, true>, 64, p, s);
+            l, marlin_decode_kernel<FMT, AT, 4, 2, 1, true, GSM, true, 2, true>, 64, p, s);
     }
     MMI_DECODE(4, 3, 4, true, false, 1)
     MMI_DECODE(4, 3, 4, true, false, 3)
@@ -54,6 +54,7 @@ static hipError_t launch_gsm(const GemmLaunch& l, const GemmParams& p, hipStream
     MMI_DECODE(4, 4, 2, true, true, 1)
     MMI_DECODE(4, 3, 1, true, true, 1)
     MMI_DECODE(4, 3, 1, true, true, 2)
+    MMI_DECODE(4, 2, 1, true, true, 2)
     MMI_DECODE(4, 4, 1, true, true, 1)
     if constexpr (FMT != FMT_MXFP4 && FMT != FMT_NVFP4 && GSM != GSM_SMALL) {
       // 16-column groups for small N at M <= 16: 16 waves split K, every step in flight
