@@ -101,3 +101,36 @@ def test_gemm_random_shapes_int_zero_points_and_act_order(i):
         ref = O.gemm_ref(a, deq)
     assert O.max_abs_rel_err(out, ref) <= TOL
 
+
+
+def _large_case(i):
+    rng = random.Random(9800 + i)
+    fmt = FORMATS[(3 * i) % len(FORMATS)]
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    gs = rng.choice(GROUPS[fmt])
+    k = 128 * rng.randint(8, 64)
+    n = 256 * rng.randint(8, 64)
+    while n * k > (24 << 20) and k > 1024:  # keeps the oracle's quantizer to a few seconds
+        k -= 128
+    m = max(1, int(round(2 ** rng.uniform(0, 8))))
+    return fmt, dtype, gs, m, n, k
+
+
+LARGE_CASES = [_large_case(i) for i in range(12)]
+
+
+@pytest.mark.parametrize("i", range(len(LARGE_CASES)))
+def test_gemm_random_large_shapes(i):
+    """Larger random shapes (N 2048-16384, K 1024-8192, M 1-256): the wide-N decode instances,
+    the split mix of whole column groups and K-split leftovers, XCD-grouped block orders and
+    the 128-row blocks at their production sizes."""
+    fmt, dtype, gs, m, n, k = LARGE_CASES[i]
+    print(f"case sweep-large {i}: fmt={fmt} dtype={dtype} gs={gs} m={m} n={n} k={k}", flush=True)
+    case = make_case(fmt, k, n, dtype, gs=gs, seed=900 + i)
+    a = torch.randn((m, k), generator=torch.Generator().manual_seed(950 + i)).to(dtype)
+    d = to_dev(case)
+    words = capi.gptq_marlin_repack(d.gptq_words, None, k, n, BITS[fmt])
+    out = capi.marlin_gemm(a.cuda(), words, d.scales, case.type_id, m, n, k,
+                           global_scale=d.global_scale, b_zeros=d.zeros,
+                           is_zp_float=d.zeros is not None).cpu()
+    assert O.max_abs_rel_err(out, O.gemm_ref(a, case.deq)) <= TOL
