@@ -169,3 +169,52 @@ def test_fused_marlin_moe_random_layers(i):
                            is_w1_zp_float=z13 is not None, is_w2_zp_float=z2 is not None).cpu()
     ref = O.moe_layer_ref(x, d13, d2, tw, ids)
     assert O.max_abs_rel_err(out, ref) <= 2 * TOL
+
+
+def _large_moe_case(i):
+    rng = random.Random(7900 + i)
+    fmt = ("u4", "u4b8", "u8b128", "mxfp4", "nvfp4", "fp8")[i % 6]
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    e = rng.randint(4, 8)
+    topk = rng.randint(2, 4)
+    t = max(1, int(round(2 ** rng.uniform(2, math.log2(600)))))
+    k = 128 * rng.randint(8, 24)
+    n = 256 * rng.randint(4, 12)
+    return fmt, dtype, e, topk, t, k, n
+
+
+LARGE_MOE_CASES = [_large_moe_case(i) for i in range(12)]
+
+
+@pytest.mark.parametrize("i", range(len(LARGE_MOE_CASES)))
+def test_moe_gemm_random_large_shapes(i):
+    """MoE GEMMs at larger K (1024-3072) and size_n (1024-3072) with up to 600 tokens: both
+    the few-routes kernel (two waves per SIMD) and the multistage blocks at sizes near the
+    production layer's, route by route against the oracle."""
+    fmt, dtype, E, topk, T, K, N = LARGE_MOE_CASES[i]
+    bs = 64 if T * topk > 16 * E else 16
+    print(f"case moe-sweep-large {i}: fmt={fmt} dtype={dtype} E={E} topk={topk} T={T} K={K} "
+          f"N={N} bs={bs}", flush=True)
+    cases = [make_case(fmt, K, N, dtype, seed=1500 + 31 * i + j) for j in range(E)]
+    words = torch.stack([capi.gptq_marlin_repack(c.gptq_words.cuda(), None, K, N, BITS[fmt])
+                         for c in cases])
+    scales = torch.stack([c.scales for c in cases]).cuda()
+    zeros = torch.stack([c.zeros for c in cases]).cuda() if cases[0].zeros is not None else None
+    glob = (torch.cat([c.global_scale for c in cases]).cuda()
+            if cases[0].global_scale is not None else None)
+    gen = torch.Generator().manual_seed(1600 + i)
+    x = torch.randn((T, K), generator=gen).to(dtype)
+    tw, ids = O.route_topk(torch.randn((T, E), generator=gen), topk)
+    s, e, npad = (torch.from_numpy(v) for v in O.moe_align_block_size(ids.numpy(), E, bs))
+    out = capi.moe_wna16_marlin_gemm(
+        x.cuda(), words, scales, s.cuda(), e.cuda(), npad.cuda(), tw.cuda(), bs, topk, True,
+        cases[0].type_id, T, N, K, b_zeros=zeros, global_scale=glob,
+        is_zp_float=zeros is not None).cpu()
+    flat = ids.reshape(-1)
+    xr = x.float()[torch.arange(flat.numel()) // topk]
+    ref = torch.empty((flat.numel(), N))
+    for ex in range(E):
+        rows = (flat == ex).nonzero().flatten()
+        ref[rows] = xr[rows] @ cases[ex].deq.float()
+    ref = ref * tw.reshape(-1, 1)
+    assert O.max_abs_rel_err(out, ref) <= TOL
