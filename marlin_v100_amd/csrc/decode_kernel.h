@@ -21,7 +21,8 @@
 //     bookkeeping waits only for the step it consumes;
 //   * OCC = 3 instances fit three waves per SIMD (activations then run one step behind the
 //     weights, and the tiles are multiplied two at a time), so a launch of up to three
-//     workgroups per CU is resident in one round;
+//     workgroups per CU is resident in one round; the few-routes MoE blocks use the same
+//     register-lean order at OCC = 2 (two one-wave workgroups per SIMD);
 //   * integer and fp8 weights use the integer-operand path (device_common.h): the MFMA B
 //     operand is the code itself and the scale / zero point is applied per group to the
 //     fp32 partial sums;
