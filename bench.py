@@ -438,7 +438,7 @@ def main() -> int:
         WARM_SECONDS = args.warm_seconds
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+                                   "(the path's multi-GPU sharding is designed, not run)"}))
         return 2
     import torch
 
